@@ -1,0 +1,176 @@
+/*
+ * pagedkv.h - C ABI of the MI355X (gfx950) paged-KV hot path.
+ *
+ * The library (libpagedkv_gfx950.so) replaces the reference's nanobind module
+ * `sglang_mlx._ext` (bindings.cpp:37-134) and the MLX host ops behind it
+ * (paged_attention/mlx_paged_attention.cpp, paged_attention/mlx_cache.cpp,
+ * paged_attention/mlx_device.cpp).  Every entry point takes plain device
+ * pointers, sizes and strides; no framework types cross this boundary.
+ *
+ * Conventions shared by all entry points
+ *   - Return value: PKV_OK (0) on success, otherwise a PKV_ERR_* code; the
+ *     message of the last failure on the calling thread is returned by
+ *     pkv_last_error().  Argument checks run before any HIP call, so a
+ *     rejected call has no side effect.
+ *   - Launches are asynchronous on `stream` (a hipStream_t passed as void*;
+ *     NULL = the legacy default stream).  Nothing synchronises.
+ *   - The library allocates no device memory.  Output buffers and the
+ *     attention workspace belong to the caller.
+ *   - Strides are in elements, not bytes.
+ *   - Block tables, context lengths and slot mappings are 32-bit integers.
+ */
+#ifndef PAGEDKV_H
+#define PAGEDKV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes.  PKV_ERR_INVALID and PKV_ERR_UNSUPPORTED map to Python
+ * ValueError (the reference raises std::invalid_argument for both,
+ * mlx_paged_attention.cpp:156-199); PKV_ERR_HIP maps to RuntimeError. */
+enum {
+  PKV_OK = 0,
+  PKV_ERR_INVALID = 1,
+  PKV_ERR_UNSUPPORTED = 2,
+  PKV_ERR_HIP = 3
+};
+
+/* Element types (reference dtypeStr, mlx_paged_attention.cpp:30-37). */
+enum { PKV_F32 = 0, PKV_F16 = 1, PKV_BF16 = 2 };
+
+/* KV cache layouts.
+ *   PKV_LAYOUT_PAGED5D    : K [num_blocks, Hkv, D/x, block_size, x],
+ *                           V [num_blocks, Hkv, D, block_size],
+ *                           x = 16 / sizeof(cache element)
+ *                           (reshape_and_cache.metal:20-23).
+ *   PKV_LAYOUT_TOKEN_MAJOR: K and V [num_slots, Hkv, D] with
+ *                           slot = block * block_size + offset; this is both
+ *                           the MHATokenPool buffer (memory_pool.py:102-108)
+ *                           and the flash layout [num_blocks, block_size,
+ *                           Hkv, D] (reshape_and_cache.metal:104-107). */
+enum { PKV_LAYOUT_PAGED5D = 0, PKV_LAYOUT_TOKEN_MAJOR = 1 };
+
+/* Library identification string (build flags and target). */
+const char* pkv_version(void);
+
+/* Message describing the last non-zero status returned on this thread. */
+const char* pkv_last_error(void);
+
+/*
+ * Slot-mapped KV append.
+ * Replaces ReshapeAndCache (mlx_cache.cpp:40-97, :256-278) for
+ * PKV_LAYOUT_PAGED5D and ReshapeAndCacheFlash (mlx_cache.cpp:101-153,
+ * :280-300) for PKV_LAYOUT_TOKEN_MAJOR; kernel semantics follow
+ * reshape_and_cache.metal:35-69 and :115-136.
+ *
+ * key/value   : [num_tokens, num_kv_heads, head_size], row stride
+ *               key_stride / value_stride; the inner [Hkv, D] is contiguous.
+ * slot_mapping: [num_tokens]; a negative slot skips the token
+ *               (reshape_and_cache.metal:36-39).  Slots >= num_slots are
+ *               skipped as well (the reference does not check them).
+ * block_size/x: used by PKV_LAYOUT_PAGED5D only; x must be
+ *               16 / sizeof(cache element).
+ * num_slots   : num_blocks * block_size (PAGED5D) or the first dimension of
+ *               the token-major buffers.
+ * kv_dtype -> cache_dtype pairs: equal types, or F32 -> F16 / F32 -> BF16
+ *               (round to nearest even; NaN -> 0x7FC0 for BF16).
+ */
+int pkv_reshape_and_cache(const void* key, const void* value,
+                          void* key_cache, void* value_cache,
+                          const int32_t* slot_mapping, int64_t num_tokens,
+                          int32_t num_kv_heads, int32_t head_size,
+                          int64_t key_stride, int64_t value_stride,
+                          int32_t layout, int32_t block_size, int32_t x,
+                          int64_t num_slots, int32_t kv_dtype,
+                          int32_t cache_dtype, void* stream);
+
+/*
+ * Scratch bytes that pkv_paged_attention needs for these sizes (per-partition
+ * (max, sum) pairs and per-partition outputs, float32).  partition_size = 0
+ * selects the single-pass (v1) semantics; the library then chooses its own
+ * internal split.  The scratch needs no initialisation.  Returns 0 for
+ * invalid sizes.
+ */
+size_t pkv_paged_attention_workspace_size(int32_t num_seqs, int32_t num_heads,
+                                          int32_t num_kv_heads,
+                                          int32_t head_size,
+                                          int32_t max_seq_len,
+                                          int32_t partition_size);
+
+/*
+ * Bytes of arrival counters (one small int32 array per sequence and head
+ * group) that pkv_paged_attention needs.  The counter buffer must be all
+ * zero the first time it is used; every call leaves it all zero again, so one
+ * zero-filled buffer (of the largest size needed) serves any number of calls
+ * ordered on one stream.  Calls that overlap in time must not share it.
+ * Returns 0 for invalid sizes.
+ */
+size_t pkv_paged_attention_counter_size(int32_t num_seqs, int32_t num_heads,
+                                        int32_t num_kv_heads);
+
+/*
+ * Block-table decode attention.
+ * Replaces PagedAttentionV1 (mlx_paged_attention.cpp:93-144, :150-213);
+ * semantics follow paged_attention_kernels.metal:37-168:
+ *   out[s,h,:] = sum_t softmax_t(scale * q[s,h].k_t + alibi[h]*(t-ctx+1)) v_t
+ * with the GQA map kv_head = h / (num_heads / num_kv_heads), the softmax
+ * denominator (sum + 1e-6), fp32 accumulation, and a zero output row when
+ * context_lens[s] == 0 or context_lens[s] > max_seq_len.
+ *
+ * partition_size = 0 : paged_attention_v1 semantics (one softmax over the
+ *                      whole context; the split is an internal detail).
+ * partition_size > 0 : split-K (paged_attention_v2): partitions of
+ *                      partition_size tokens, merged by log-sum-exp.  Must be
+ *                      a multiple of 16 and of block_size, at most 1024.
+ * query   : [num_seqs, num_heads, head_size], row stride q_stride.
+ * out     : [num_seqs, num_heads, head_size] contiguous, same dtype as query.
+ * block_tables: [num_seqs, max_num_blocks_per_seq]; entries past
+ *               ceil(ctx / block_size) are never read.  Entries outside
+ *               [0, num_blocks) mask their tokens out.
+ * alibi_slopes: [num_heads] float32 or NULL.
+ * Cache strides: k_block_stride/k_head_stride (and v_*) are the strides of
+ *               the block and head dimensions (PAGED5D).  TOKEN_MAJOR is not
+ *               accepted by this entry point yet (PKV_ERR_UNSUPPORTED).
+ * (q_dtype, cache_dtype): (BF16,BF16), (F16,F16), (F32,BF16), (F32,F16).
+ * head_size in {32,64,80,96,112,120,128,192,256}; block_size in {8,16,32}
+ * (isValidConfig, mlx_paged_attention.cpp:52-59).
+ */
+int pkv_paged_attention(void* out, const void* query, const void* key_cache,
+                        const void* value_cache, const int32_t* block_tables,
+                        const int32_t* context_lens,
+                        const float* alibi_slopes, int32_t num_seqs,
+                        int32_t num_heads, int32_t num_kv_heads,
+                        int32_t head_size, int32_t block_size,
+                        int32_t max_num_blocks_per_seq, int32_t max_seq_len,
+                        int64_t num_blocks, float scale, int64_t q_stride,
+                        int64_t k_block_stride, int64_t k_head_stride,
+                        int64_t v_block_stride, int64_t v_head_stride,
+                        int32_t layout, int32_t partition_size,
+                        void* workspace, size_t workspace_bytes,
+                        int32_t* counters, size_t counter_bytes,
+                        int32_t q_dtype, int32_t cache_dtype, void* stream);
+
+/*
+ * LDS bytes available to one workgroup on a device.
+ * Replaces get_max_shared_memory_per_block_device_attribute
+ * (mlx_device.cpp:16-20, bindings.cpp:130-133).
+ */
+int pkv_max_shared_memory_per_block(int32_t device_id, int64_t* out);
+
+/*
+ * hipDeviceGetAttribute passthrough.  Replaces get_device_attribute
+ * (mlx_device.cpp:12-14, bindings.cpp:125-128), which always throws in the
+ * reference; here `attribute` is a hipDeviceAttribute_t value.
+ */
+int pkv_get_device_attribute(int32_t attribute, int32_t device_id,
+                             int64_t* out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PAGEDKV_H */

@@ -1,0 +1,316 @@
+"""CPU oracle for the paged-KV hot path -- TEST INFRASTRUCTURE ONLY.
+
+This module restates the reference's algorithms in NumPy so that tests,
+``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` can
+check the HIP kernels.  Nothing in the product package imports it; the
+product path fails loudly when its HIP library is missing instead of falling
+back to anything here.
+
+Representation: 16-bit caches are carried as ``uint16`` bit arrays together
+with a dtype name (``"float16"`` / ``"bfloat16"``); float32 data as
+``float32``.  The append functions work on those raw arrays (bit-exact); the
+attention functions decode to float64 and compute in float64.
+
+Functions and the reference code they restate (paths relative to the
+reference repository):
+
+- ``f32_to_bf16_bits``     paged_attention/metal/utils.metal:21-35
+- ``convert_elements``     paged_attention/metal/cache/reshape_and_cache.metal:9-12
+- ``reshape_and_cache_paged5d``
+                           reshape_and_cache.metal:35-69;
+                           tests/test_paged_attention_kernel.py:33-65
+- ``reshape_and_cache_token_major``
+                           reshape_and_cache.metal:115-136;
+                           sglang_mlx/srt/mem_cache/memory_pool.py:117-137
+- ``paged_attention``      paged_attention/metal/attention/paged_attention_kernels.metal:37-168;
+                           tests/test_paged_attention_kernel.py:68-120
+- ``paged_attention_split``  (no reference code: split-K is absent from the
+                           reference, README.md:11-19) log-sum-exp merge of
+                           per-partition (max, sum, output).
+- ``gather_kv``            the per-token gather of test_paged_attention_kernel.py:93-105
+
+Pinning (tests/test_oracle_*.py): bf16/fp16 rounding against torch's
+conversions; the append against the element loop of the reference's own test
+and read-back invariants; attention against torch's float64
+scaled_dot_product_attention, closed forms (single token, equal keys,
+one-hot logits, ALiBi geometric weights) and the reference's zero-output
+cases; split-K against the unpartitioned oracle.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+# ---------------------------------------------------------------------------
+# Element conversions (bit level)
+# ---------------------------------------------------------------------------
+
+DTYPES = ("float32", "float16", "bfloat16")
+
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """float32 -> bfloat16 bits: round to nearest even, every NaN -> 0x7FC0.
+
+    Restates float_to_bfloat_bits, paged_attention/metal/utils.metal:21-35.
+    """
+    u = np.asarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) & 0xFFFF
+    return np.where(nan, 0x7FC0, r).astype(np.uint16)
+
+
+def bf16_bits_to_f32(b: np.ndarray) -> np.ndarray:
+    """bfloat16 bits -> float32 (upper half of the float word), utils.metal:37-40."""
+    return (np.asarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f16_bits_to_f32(b: np.ndarray) -> np.ndarray:
+    return np.asarray(b, dtype=np.uint16).view(np.float16).astype(np.float32)
+
+
+def f32_to_f16_bits(x: np.ndarray) -> np.ndarray:
+    """float32 -> IEEE binary16 bits, round to nearest even (NumPy's cast)."""
+    return np.asarray(x, dtype=np.float32).astype(np.float16).view(np.uint16)
+
+
+def to_storage(x: np.ndarray, dtype: str) -> np.ndarray:
+    """Round float data to the storage representation of ``dtype``."""
+    x = np.asarray(x, dtype=np.float32)
+    if dtype == "float32":
+        return x.copy()
+    if dtype == "float16":
+        return f32_to_f16_bits(x)
+    if dtype == "bfloat16":
+        return f32_to_bf16_bits(x)
+    raise ValueError(dtype)
+
+
+def decode(bits: np.ndarray, dtype: str) -> np.ndarray:
+    """Storage representation -> float64 values."""
+    if dtype == "float32":
+        return np.asarray(bits, dtype=np.float32).astype(np.float64)
+    if dtype == "float16":
+        return f16_bits_to_f32(bits).astype(np.float64)
+    if dtype == "bfloat16":
+        return bf16_bits_to_f32(bits).astype(np.float64)
+    raise ValueError(dtype)
+
+
+def convert_elements(src: np.ndarray, src_dtype: str, dst_dtype: str) -> np.ndarray:
+    """static_cast<CACHE_T>(KV_T), reshape_and_cache.metal:9-12.
+
+    Equal types copy the bits; float32 -> float16/bfloat16 rounds to nearest
+    even.  The reference instantiates exactly these pairs
+    (reshape_and_cache.metal:91-95).
+    """
+    if src_dtype == dst_dtype:
+        return np.array(src, copy=True)
+    if src_dtype != "float32":
+        raise ValueError(f"unsupported conversion {src_dtype} -> {dst_dtype}")
+    return to_storage(src, dst_dtype)
+
+
+# ---------------------------------------------------------------------------
+# Append
+# ---------------------------------------------------------------------------
+
+
+def reshape_and_cache_paged5d(key, value, key_cache, value_cache, slot_mapping,
+                              kv_dtype: str, cache_dtype: str):
+    """Scatter new tokens into the paged 5-D layout; returns new caches.
+
+    key/value: [N, H, D] storage arrays.  key_cache [nb, H, D/x, bs, x],
+    value_cache [nb, H, D, bs].  Token i goes to block slot//bs, offset
+    slot%bs; slots < 0 are skipped (reshape_and_cache.metal:35-69).
+    Implemented with vectorised fancy indexing; the reference test's element
+    loop (test_paged_attention_kernel.py:46-63) is the independent check.
+    """
+    kc = np.array(key_cache, copy=True)
+    vc = np.array(value_cache, copy=True)
+    nb, H, dx, bs, x = kc.shape
+    D = dx * x
+    slots = np.asarray(slot_mapping).astype(np.int64)
+    keep = slots >= 0
+    tok = np.nonzero(keep)[0]
+    if tok.size == 0:
+        return kc, vc
+    s = slots[keep]
+    blk, off = s // bs, s % bs
+    k = convert_elements(np.asarray(key)[tok], kv_dtype, cache_dtype)  # [n, H, D]
+    v = convert_elements(np.asarray(value)[tok], kv_dtype, cache_dtype)
+    # Two tokens naming one slot race on the GPU (the reference does not
+    # order them either); the oracle lets the later token win.
+    order = np.arange(tok.size)
+    _, last = np.unique(s[::-1], return_index=True)
+    sel = order[::-1][last]
+    blk, off, k, v = blk[sel], off[sel], k[sel], v[sel]
+    d = np.arange(D)
+    kc[blk[:, None, None], np.arange(H)[None, :, None], (d // x)[None, None, :],
+       off[:, None, None], (d % x)[None, None, :]] = k
+    vc[blk[:, None, None], np.arange(H)[None, :, None], d[None, None, :],
+       off[:, None, None]] = v
+    return kc, vc
+
+
+def reshape_and_cache_token_major(key, value, key_cache, value_cache, slot_mapping,
+                                  kv_dtype: str, cache_dtype: str):
+    """Scatter into [num_slots, H, D] (MHATokenPool / flash layout).
+
+    reshape_and_cache.metal:115-136 with slot = block*bs + offset, which is
+    the MHATokenPool buffer indexing of memory_pool.py:117-137.
+    """
+    kc = np.array(key_cache, copy=True)
+    vc = np.array(value_cache, copy=True)
+    shape = kc.shape
+    kc = kc.reshape(-1, shape[-2], shape[-1])
+    vc = vc.reshape(-1, shape[-2], shape[-1])
+    slots = np.asarray(slot_mapping).astype(np.int64)
+    tok = np.nonzero(slots >= 0)[0]
+    if tok.size:
+        s = slots[tok]
+        _, last = np.unique(s[::-1], return_index=True)
+        sel = np.arange(tok.size)[::-1][last]
+        kc[s[sel]] = convert_elements(np.asarray(key)[tok[sel]], kv_dtype, cache_dtype)
+        vc[s[sel]] = convert_elements(np.asarray(value)[tok[sel]], kv_dtype, cache_dtype)
+    return kc.reshape(shape), vc.reshape(shape)
+
+
+# ---------------------------------------------------------------------------
+# Attention
+# ---------------------------------------------------------------------------
+
+
+def gather_kv(kc64: np.ndarray, vc64: np.ndarray, block_row: np.ndarray, ctx: int):
+    """Logical tokens 0..ctx-1 of one sequence -> (K, V) as [ctx, H, D].
+
+    kc64 [nb, H, D/x, bs, x] and vc64 [nb, H, D, bs] hold decoded values.
+    Token t lives in block block_row[t // bs] at offset t % bs
+    (test_paged_attention_kernel.py:93-105).
+    """
+    nb, H, dx, bs, x = kc64.shape
+    t = np.arange(ctx)
+    blk = np.asarray(block_row, dtype=np.int64)[t // bs]
+    off = t % bs
+    k = kc64[blk, :, :, off, :].reshape(ctx, H, dx * x)  # [ctx, H, D/x, x] -> [ctx, H, D]
+    v = vc64[blk, :, :, off]                              # [ctx, H, D]
+    return k, v
+
+
+def _softmax_attend(qh: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float,
+                    bias: np.ndarray | None):
+    """One sequence, all heads: qh [Hq, D]; k, v [T, Hkv, D] -> [Hq, D].
+
+    Query head h reads KV head h // (Hq/Hkv) (paged_attention_kernels.metal:57-58);
+    scale, then ALiBi (:95-97), max-subtracted exp, denominator
+    (sum + 1e-6) (:144), weighted V sum (:146-160).
+    """
+    Hq, D = qh.shape
+    Hkv = k.shape[1]
+    qg = qh.reshape(Hkv, Hq // Hkv, D)
+    logits = np.einsum("kgd,tkd->kgt", qg, k) * scale
+    if bias is not None:
+        logits = logits + bias.reshape(Hkv, Hq // Hkv, -1)
+    m = logits.max(axis=2, keepdims=True)
+    p = np.exp(logits - m)
+    inv = 1.0 / (p.sum(axis=2, keepdims=True) + 1e-6)
+    return np.einsum("kgt,tkd->kgd", p * inv, v).reshape(Hq, D)
+
+
+def alibi_bias(slopes: np.ndarray, ctx: int) -> np.ndarray:
+    """slope[h] * (t - ctx + 1), paged_attention_kernels.metal:97."""
+    t = np.arange(ctx)
+    return np.asarray(slopes, dtype=np.float64)[:, None] * (t - ctx + 1)[None, :]
+
+
+def paged_attention(q, key_cache, value_cache, block_tables, context_lens, num_kv_heads: int,
+                    scale: float, block_size: int, max_seq_len: int, alibi_slopes=None,
+                    q_dtype: str = "float32", cache_dtype: str = "float32") -> np.ndarray:
+    """paged_attention_v1 in float64 -> [B, Hq, D] float64.
+
+    Follows paged_attention_kernels.metal:37-168: zero output when
+    ctx == 0 or ctx > max_seq_len (:44-50, context read as uint32),
+    GQA map h // (Hq/Hkv) (:57-58), fp32-exact inputs, denominator
+    sum + 1e-6 (:144).  ``block_size`` is implied by the cache shape and
+    only cross-checked.
+    """
+    q64 = decode(q, q_dtype)
+    kc64 = decode(key_cache, cache_dtype)
+    vc64 = decode(value_cache, cache_dtype)
+    assert kc64.shape[3] == block_size
+    B, Hq, D = q64.shape
+    assert Hq % num_kv_heads == 0
+    out = np.zeros((B, Hq, D), dtype=np.float64)
+    lens = np.asarray(context_lens).astype(np.int64) & 0xFFFFFFFF
+    for s in range(B):
+        ctx = int(lens[s])
+        if ctx == 0 or ctx > max_seq_len:
+            continue
+        k, v = gather_kv(kc64, vc64, block_tables[s], ctx)
+        bias = None if alibi_slopes is None else alibi_bias(alibi_slopes, ctx)
+        out[s] = _softmax_attend(q64[s], k, v, scale, bias)
+    return out
+
+
+def partition_stats(qh, k, v, scale, bias, lo: int, hi: int):
+    """(max, sum, normalised output) of tokens [lo, hi) for all heads."""
+    Hq, D = qh.shape
+    Hkv = k.shape[1]
+    qg = qh.reshape(Hkv, Hq // Hkv, D)
+    logits = np.einsum("kgd,tkd->kgt", qg, k[lo:hi]).reshape(Hq, hi - lo) * scale
+    if bias is not None:
+        logits = logits + bias[:, lo:hi]
+    m = logits.max(axis=1)
+    p = np.exp(logits - m[:, None])
+    s = p.sum(axis=1)
+    o = np.einsum("kgt,tkd->kgd", p.reshape(Hkv, Hq // Hkv, -1), v[lo:hi]).reshape(Hq, D) / s[:, None]
+    return m, s, o
+
+
+def lse_merge(ms: np.ndarray, ss: np.ndarray, os_: np.ndarray) -> np.ndarray:
+    """Merge partitions: M = max m_p, S = sum s_p e^(m_p-M),
+    O = sum o_p s_p e^(m_p-M) / (S + 1e-6).  ms, ss [P, H]; os_ [P, H, D]."""
+    M = ms.max(axis=0)
+    w = ss * np.exp(ms - M[None, :])
+    return np.einsum("ph,phd->hd", w, os_) / (w.sum(axis=0) + 1e-6)[:, None]
+
+
+def paged_attention_split(q, key_cache, value_cache, block_tables, context_lens,
+                          num_kv_heads: int, scale: float, block_size: int, max_seq_len: int,
+                          partition_size: int, alibi_slopes=None, q_dtype: str = "float32",
+                          cache_dtype: str = "float32") -> np.ndarray:
+    """Split-K decode: partitions of ``partition_size`` tokens, LSE-merged.
+
+    Same edge semantics as ``paged_attention``; equal to it up to float64
+    rounding (the merge is an algebraic identity).
+    """
+    q64 = decode(q, q_dtype)
+    kc64 = decode(key_cache, cache_dtype)
+    vc64 = decode(value_cache, cache_dtype)
+    B, Hq, D = q64.shape
+    out = np.zeros((B, Hq, D), dtype=np.float64)
+    lens = np.asarray(context_lens).astype(np.int64) & 0xFFFFFFFF
+    for s in range(B):
+        ctx = int(lens[s])
+        if ctx == 0 or ctx > max_seq_len:
+            continue
+        k, v = gather_kv(kc64, vc64, block_tables[s], ctx)
+        bias = None if alibi_slopes is None else alibi_bias(alibi_slopes, ctx)
+        parts = [partition_stats(q64[s], k, v, scale, bias, lo, min(lo + partition_size, ctx))
+                 for lo in range(0, ctx, partition_size)]
+        out[s] = lse_merge(np.stack([p[0] for p in parts]), np.stack([p[1] for p in parts]),
+                           np.stack([p[2] for p in parts]))
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Layout helpers for tests: token-major <-> paged 5-D
+# ---------------------------------------------------------------------------
+
+
+def token_major_to_paged5d(kt: np.ndarray, vt: np.ndarray, block_size: int, x: int):
+    """[num_slots, H, D] (slot = block*bs + off) -> paged 5-D K and V."""
+    S, H, D = kt.shape
+    nb = S // block_size
+    k5 = kt.reshape(nb, block_size, H, D // x, x).transpose(0, 2, 3, 1, 4).copy()
+    v4 = vt.reshape(nb, block_size, H, D).transpose(0, 2, 3, 1).copy()
+    return k5, v4

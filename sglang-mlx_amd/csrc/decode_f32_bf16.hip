@@ -1,0 +1,8 @@
+// Decode-kernel instantiations for query type F32 and cache type BF16 (every
+// supported head size and block size).  One translation unit per type pair
+// keeps the kernel matrix compiling in parallel.
+#include "paged_decode_impl.h"
+
+namespace pkv {
+template hipError_t launch_decode_typed<F32, BF16>(const DecodeParams&, int, int, hipStream_t, bool*);
+}  // namespace pkv

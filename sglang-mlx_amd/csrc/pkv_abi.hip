@@ -1,0 +1,273 @@
+// extern "C" entry points of libpagedkv_gfx950.so (declared in
+// include/pagedkv.h).  They check arguments before any HIP call, size the
+// decode workspace, pick the kernel instantiation and launch it on the
+// caller's stream.  Nothing here allocates device memory or synchronises.
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+
+#include "../../include/pagedkv.h"
+#include "pkv_launch.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* where) {
+  return fail(PKV_ERR_HIP, std::string(where) + ": " + hipGetErrorString(e));
+}
+
+int elem_bytes(int32_t dt) { return dt == PKV_F32 ? 4 : 2; }
+bool valid_dtype(int32_t dt) { return dt == PKV_F32 || dt == PKV_F16 || dt == PKV_BF16; }
+bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
+
+// Supported decode shapes (isValidConfig, mlx_paged_attention.cpp:52-59).
+bool valid_head_size(int32_t d) {
+  static const int hs[] = {32, 64, 80, 96, 112, 120, 128, 192, 256};
+  for (int v : hs)
+    if (v == d) return true;
+  return false;
+}
+bool valid_block_size(int32_t b) { return b == 8 || b == 16 || b == 32; }
+
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Partition used for the single-pass (v1) semantics: 512 tokens, halved
+// while the grid would hold fewer than 2048 workgroups, doubled while one
+// sequence would need more than kMaxParts partitions.
+int32_t v1_partition(int32_t num_seqs, int32_t units, int32_t max_seq_len) {
+  int32_t ps = 512;
+  while (ps > 256 && (int64_t)num_seqs * units * ceil_div(max_seq_len, ps) < 2048) ps /= 2;
+  while (ceil_div(max_seq_len, ps) > pkv::kMaxParts && ps < pkv::kMaxPartition) ps *= 2;
+  return ps;
+}
+
+// Resolves the partition size and the partition count; returns a status.
+int resolve_partition(int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads, int32_t max_seq_len,
+                      int32_t block_size, int32_t partition_size, int32_t* ps_out, int32_t* parts_out) {
+  if (num_seqs < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
+    return fail(PKV_ERR_INVALID, "num_heads must be divisible by num_kv_heads");
+  if (max_seq_len <= 0) return fail(PKV_ERR_INVALID, "max_seq_len must be positive");
+  const int32_t group = num_heads / num_kv_heads;
+  const int32_t units = num_kv_heads * ((group + 15) / 16);
+  int32_t ps = partition_size;
+  if (ps == 0) {
+    ps = v1_partition(num_seqs, units, max_seq_len);
+  } else if (ps < 0 || ps % pkv::kTile != 0 || (block_size > 0 && ps % block_size != 0) ||
+             ps > pkv::kMaxPartition) {
+    return fail(PKV_ERR_INVALID,
+                "partition_size must be a positive multiple of 16 and of block_size, at most 1024");
+  }
+  const int64_t parts = ceil_div(max_seq_len, ps);
+  if (parts > pkv::kMaxParts)
+    return fail(PKV_ERR_UNSUPPORTED, "max_seq_len / partition_size exceeds 1024 partitions");
+  *ps_out = ps;
+  *parts_out = (int32_t)parts;
+  return PKV_OK;
+}
+
+}  // namespace
+
+namespace pkv {
+DecodeWorkspace decode_workspace_layout(int32_t num_seqs, int32_t num_heads, int32_t head_size,
+                                        int32_t max_parts) {
+  DecodeWorkspace w;
+  auto align = [](size_t x) { return (x + 255) & ~size_t(255); };
+  w.ml_bytes = align((size_t)num_seqs * num_heads * max_parts * 2 * sizeof(float));
+  w.o_bytes = align((size_t)num_seqs * num_heads * max_parts * head_size * sizeof(float));
+  w.total = w.ml_bytes + w.o_bytes;
+  return w;
+}
+size_t decode_counter_bytes(int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads) {
+  const int32_t group = num_heads / num_kv_heads;
+  const int32_t units = num_kv_heads * ((group + 15) / 16);
+  return (size_t)num_seqs * units * (1 + kMaxGroups) * sizeof(int32_t);
+}
+}  // namespace pkv
+
+extern "C" {
+
+const char* pkv_version(void) { return "pagedkv gfx950 (hipcc -O3, wave64, MFMA 16x16x32/16x16x16)"; }
+
+const char* pkv_last_error(void) { return g_last_error.c_str(); }
+
+int pkv_reshape_and_cache(const void* key, const void* value, void* key_cache, void* value_cache,
+                          const int32_t* slot_mapping, int64_t num_tokens, int32_t num_kv_heads,
+                          int32_t head_size, int64_t key_stride, int64_t value_stride, int32_t layout,
+                          int32_t block_size, int32_t x, int64_t num_slots, int32_t kv_dtype,
+                          int32_t cache_dtype, void* stream) {
+  if (num_tokens < 0) return fail(PKV_ERR_INVALID, "num_tokens must be non-negative");
+  if (num_kv_heads <= 0 || head_size <= 0) return fail(PKV_ERR_INVALID, "num_kv_heads and head_size must be positive");
+  if (!valid_dtype(kv_dtype) || !valid_dtype(cache_dtype)) return fail(PKV_ERR_INVALID, "Unsupported dtype");
+  if (!(kv_dtype == cache_dtype || (kv_dtype == PKV_F32 && cache_dtype != PKV_F32)))
+    return fail(PKV_ERR_UNSUPPORTED, "Unsupported key/cache dtype pair");
+  if (layout != PKV_LAYOUT_PAGED5D && layout != PKV_LAYOUT_TOKEN_MAJOR)
+    return fail(PKV_ERR_INVALID, "Unknown cache layout");
+  if (num_slots <= 0 || num_slots > INT32_MAX) return fail(PKV_ERR_INVALID, "num_slots must be in [1, 2^31)");
+  const int64_t row = (int64_t)num_kv_heads * head_size;
+  if (key_stride < row || value_stride < row)
+    return fail(PKV_ERR_INVALID, "key/value row stride is smaller than num_kv_heads * head_size");
+  if (layout == PKV_LAYOUT_PAGED5D) {
+    if (block_size <= 0) return fail(PKV_ERR_INVALID, "block_size must be positive");
+    if (x != 16 / elem_bytes(cache_dtype))
+      return fail(PKV_ERR_INVALID, "key_cache last dimension must be 16 / sizeof(cache element)");
+    if (head_size % x != 0) return fail(PKV_ERR_INVALID, "head_size must be a multiple of x");
+    if (num_slots % block_size != 0) return fail(PKV_ERR_INVALID, "num_slots must be a multiple of block_size");
+  }
+  if (num_tokens == 0) return PKV_OK;
+  if (!key || !value || !key_cache || !value_cache || !slot_mapping)
+    return fail(PKV_ERR_INVALID, "null buffer");
+  const int kb = elem_bytes(kv_dtype);
+  const bool aligned = aligned16(key) && aligned16(value) && aligned16(key_cache) && aligned16(value_cache) &&
+                       (key_stride * kb) % 16 == 0 && (value_stride * kb) % 16 == 0 &&
+                       (layout == PKV_LAYOUT_TOKEN_MAJOR || (head_size * kb) % 16 == 0);
+  pkv::RacParams p;
+  p.key = key;
+  p.value = value;
+  p.key_cache = key_cache;
+  p.value_cache = value_cache;
+  p.slot_mapping = slot_mapping;
+  p.num_tokens = num_tokens;
+  p.key_stride = key_stride;
+  p.value_stride = value_stride;
+  p.num_slots = num_slots;
+  p.num_heads = num_kv_heads;
+  p.head_size = head_size;
+  p.block_size = layout == PKV_LAYOUT_PAGED5D ? block_size : 1;
+  p.layout = layout;
+  p.kv_dtype = kv_dtype;
+  p.cache_dtype = cache_dtype;
+  const hipError_t e = pkv::launch_reshape_and_cache(p, aligned, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "reshape_and_cache launch");
+  return PKV_OK;
+}
+
+size_t pkv_paged_attention_workspace_size(int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
+                                          int32_t head_size, int32_t max_seq_len, int32_t partition_size) {
+  int32_t ps = 0, parts = 0;
+  if (head_size <= 0) return 0;
+  if (resolve_partition(num_seqs, num_heads, num_kv_heads, max_seq_len, 0, partition_size, &ps, &parts) != PKV_OK)
+    return 0;
+  return pkv::decode_workspace_layout(num_seqs, num_heads, head_size, parts).total;
+}
+
+size_t pkv_paged_attention_counter_size(int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads) {
+  if (num_seqs < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0) return 0;
+  return pkv::decode_counter_bytes(num_seqs, num_heads, num_kv_heads);
+}
+
+int pkv_paged_attention(void* out, const void* query, const void* key_cache, const void* value_cache,
+                        const int32_t* block_tables, const int32_t* context_lens, const float* alibi_slopes,
+                        int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads, int32_t head_size,
+                        int32_t block_size, int32_t max_num_blocks_per_seq, int32_t max_seq_len,
+                        int64_t num_blocks, float scale, int64_t q_stride, int64_t k_block_stride,
+                        int64_t k_head_stride, int64_t v_block_stride, int64_t v_head_stride, int32_t layout,
+                        int32_t partition_size, void* workspace, size_t workspace_bytes, int32_t* counters,
+                        size_t counter_bytes, int32_t q_dtype, int32_t cache_dtype, void* stream) {
+  if (num_seqs < 0) return fail(PKV_ERR_INVALID, "num_seqs must be non-negative");
+  int32_t ps = 0, parts = 0;
+  const int st = resolve_partition(num_seqs, num_heads, num_kv_heads, max_seq_len, block_size, partition_size,
+                                   &ps, &parts);
+  if (st != PKV_OK) return st;
+  if (max_num_blocks_per_seq <= 0 || (int64_t)max_seq_len > (int64_t)max_num_blocks_per_seq * block_size)
+    return fail(PKV_ERR_INVALID, "max_seq_len exceeds block table capacity");
+  if (!valid_head_size(head_size) || !valid_block_size(block_size))
+    return fail(PKV_ERR_UNSUPPORTED, "Unsupported head_size/block_size for paged_attention");
+  if (layout != PKV_LAYOUT_PAGED5D)
+    return fail(PKV_ERR_UNSUPPORTED, "paged_attention supports the paged 5-D cache layout only");
+  const bool pair_ok = (q_dtype == PKV_BF16 && cache_dtype == PKV_BF16) ||
+                       (q_dtype == PKV_F16 && cache_dtype == PKV_F16) ||
+                       (q_dtype == PKV_F32 && (cache_dtype == PKV_BF16 || cache_dtype == PKV_F16));
+  if (!pair_ok) return fail(PKV_ERR_UNSUPPORTED, "Unsupported query/cache dtype pair for paged_attention");
+  if (num_blocks <= 0) return fail(PKV_ERR_INVALID, "num_blocks must be positive");
+  if (num_seqs == 0) return PKV_OK;
+  if (!out || !query || !key_cache || !value_cache || !block_tables || !context_lens)
+    return fail(PKV_ERR_INVALID, "null buffer");
+  const int qb = elem_bytes(q_dtype);
+  if (!aligned16(query) || (q_stride * qb) % 16 != 0 || q_stride < (int64_t)num_heads * head_size)
+    return fail(PKV_ERR_INVALID, "query rows must be 16-byte aligned with stride >= num_heads * head_size");
+  if (!aligned16(key_cache) || (k_block_stride * 2) % 16 != 0 || (k_head_stride * 2) % 16 != 0 ||
+      (reinterpret_cast<uintptr_t>(value_cache) & 7u) != 0 || (v_block_stride * 2) % 8 != 0 ||
+      (v_head_stride * 2) % 8 != 0)
+    return fail(PKV_ERR_INVALID, "cache base or strides are not aligned for vector loads");
+  const pkv::DecodeWorkspace w = pkv::decode_workspace_layout(num_seqs, num_heads, head_size, parts);
+  if (parts > 1) {
+    if (workspace == nullptr || workspace_bytes < w.total)
+      return fail(PKV_ERR_INVALID, "workspace is smaller than pkv_paged_attention_workspace_size()");
+    if (counters == nullptr || counter_bytes < pkv::decode_counter_bytes(num_seqs, num_heads, num_kv_heads))
+      return fail(PKV_ERR_INVALID, "counter buffer is smaller than pkv_paged_attention_counter_size()");
+    if (!aligned16(workspace) || !aligned16(counters))
+      return fail(PKV_ERR_INVALID, "workspace and counters must be 16-byte aligned");
+  }
+
+  pkv::DecodeParams p;
+  char* ws = static_cast<char*>(workspace);
+  p.out = out;
+  p.q = query;
+  p.k_cache = key_cache;
+  p.v_cache = value_cache;
+  p.block_tables = block_tables;
+  p.context_lens = context_lens;
+  p.alibi = alibi_slopes;
+  p.ws_count = counters;
+  p.ws_ml = ws ? reinterpret_cast<float*>(ws) : nullptr;
+  p.ws_o = ws ? reinterpret_cast<float*>(ws + w.ml_bytes) : nullptr;
+  p.num_blocks = num_blocks;
+  p.q_stride = q_stride;
+  p.k_block_stride = k_block_stride;
+  p.k_head_stride = k_head_stride;
+  p.v_block_stride = v_block_stride;
+  p.v_head_stride = v_head_stride;
+  p.scale_log2 = scale * 1.4426950408889634f;
+  p.num_seqs = num_seqs;
+  p.num_heads = num_heads;
+  p.num_kv_heads = num_kv_heads;
+  p.group = num_heads / num_kv_heads;
+  p.slices = (p.group + 15) / 16;
+  p.units = num_kv_heads * p.slices;
+  p.max_blocks_per_seq = max_num_blocks_per_seq;
+  p.max_seq_len = max_seq_len;
+  p.partition = ps;
+  p.max_parts = parts;
+
+  bool ok = true;
+  hipError_t e = hipErrorInvalidValue;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (q_dtype == PKV_BF16)
+    e = pkv::launch_decode_typed<pkv::BF16, pkv::BF16>(p, head_size, block_size, s, &ok);
+  else if (q_dtype == PKV_F16)
+    e = pkv::launch_decode_typed<pkv::F16, pkv::F16>(p, head_size, block_size, s, &ok);
+  else if (cache_dtype == PKV_BF16)
+    e = pkv::launch_decode_typed<pkv::F32, pkv::BF16>(p, head_size, block_size, s, &ok);
+  else
+    e = pkv::launch_decode_typed<pkv::F32, pkv::F16>(p, head_size, block_size, s, &ok);
+  if (!ok) return fail(PKV_ERR_UNSUPPORTED, "Unsupported head_size/block_size for paged_attention");
+  if (e != hipSuccess) return hip_fail(e, "paged_attention launch");
+  return PKV_OK;
+}
+
+int pkv_max_shared_memory_per_block(int32_t device_id, int64_t* out) {
+  if (!out) return fail(PKV_ERR_INVALID, "null output pointer");
+  int v = 0;
+  const hipError_t e = hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, device_id);
+  if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute");
+  *out = v;
+  return PKV_OK;
+}
+
+int pkv_get_device_attribute(int32_t attribute, int32_t device_id, int64_t* out) {
+  if (!out) return fail(PKV_ERR_INVALID, "null output pointer");
+  int v = 0;
+  const hipError_t e = hipDeviceGetAttribute(&v, static_cast<hipDeviceAttribute_t>(attribute), device_id);
+  if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute");
+  *out = v;
+  return PKV_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,90 @@
+// Parameter blocks and launcher declarations shared by the kernels and the
+// C-ABI entry points (pkv_abi.hip).  Kernels receive these structs by value
+// as kernel arguments.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <type_traits>
+
+namespace pkv {
+
+enum { kF32 = 0, kF16 = 1, kBF16 = 2 };
+
+// Largest split-K partition and the tile height of the decode kernel.
+constexpr int kMaxPartition = 1024;
+constexpr int kTile = 16;
+// Partitions merged per first-level group, and the second-level fan-in;
+// together they bound the partitions of one sequence to 16 * 64 = 1024.
+constexpr int kGroup = 16;
+constexpr int kMaxGroups = 64;
+constexpr int kMaxParts = kGroup * kMaxGroups;
+
+struct RacParams {
+  const void* key;
+  const void* value;
+  void* key_cache;
+  void* value_cache;
+  const int32_t* slot_mapping;
+  int64_t num_tokens;
+  int64_t key_stride;
+  int64_t value_stride;
+  int64_t num_slots;
+  int32_t num_heads;
+  int32_t head_size;
+  int32_t block_size;
+  int32_t layout;  // 0 = paged 5-D, 1 = token-major
+  int32_t kv_dtype;
+  int32_t cache_dtype;
+};
+
+hipError_t launch_reshape_and_cache(const RacParams& p, bool aligned, hipStream_t stream);
+
+struct DecodeParams {
+  void* out;                  // [B, Hq, D], query dtype
+  const void* q;              // [B, Hq, D], row stride q_stride
+  const void* k_cache;        // paged 5-D K
+  const void* v_cache;        // paged 5-D V
+  const int32_t* block_tables;
+  const int32_t* context_lens;
+  const float* alibi;         // [Hq] or null
+  float* ws_ml;               // [B, Hq, max_parts, 2]: (max, sum) per partition, log2 domain
+  float* ws_o;                // [B, Hq, max_parts, D]: normalised partition outputs
+  int32_t* ws_count;          // [B, units, 1 + kMaxGroups]: arrival counters, zero between calls
+  int64_t num_blocks;
+  int64_t q_stride;
+  int64_t k_block_stride, k_head_stride;
+  int64_t v_block_stride, v_head_stride;
+  float scale_log2;           // scale * log2(e)
+  int32_t num_seqs;
+  int32_t num_heads;
+  int32_t num_kv_heads;
+  int32_t group;              // num_heads / num_kv_heads
+  int32_t slices;             // ceil(group / 16): 16-head slices per KV head
+  int32_t units;              // num_kv_heads * slices
+  int32_t max_blocks_per_seq;
+  int32_t max_seq_len;
+  int32_t partition;          // tokens per partition (multiple of 16 and block_size)
+  int32_t max_parts;          // ceil(max_seq_len / partition)
+};
+
+// Scratch carve-up shared by the size query and the launcher.  The arrival
+// counters live in a separate, caller-zeroed buffer of decode_counter_bytes().
+struct DecodeWorkspace {
+  size_t ml_bytes, o_bytes, total;
+};
+DecodeWorkspace decode_workspace_layout(int32_t num_seqs, int32_t num_heads, int32_t head_size,
+                                        int32_t max_parts);
+size_t decode_counter_bytes(int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads);
+
+struct F32;
+struct F16;
+struct BF16;
+// Defined in paged_decode_impl.h, instantiated once per (query, cache) type
+// pair in decode_<q>_<cache>.hip.  *ok is cleared for an unsupported
+// head_size / block_size.
+template <class QT, class CT>
+hipError_t launch_decode_typed(const DecodeParams& p, int head_size, int block_size, hipStream_t stream,
+                               bool* ok);
+
+}  // namespace pkv

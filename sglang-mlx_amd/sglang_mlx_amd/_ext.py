@@ -1,0 +1,308 @@
+"""Boundary module: the functions of the reference's ``sglang_mlx._ext``
+(bindings.cpp:37-134) over PyTorch-ROCm tensors, backed by the gfx950 C ABI.
+
+Argument checks mirror the reference host ops (mlx_paged_attention.cpp:156-199)
+with the same messages and exception types and run before anything touches a
+GPU, so they behave the same on CPU tensors.  Kernels launch asynchronously
+on the current HIP stream of the tensors' device, as MLX's lazy evaluation
+does on its GPU stream.
+
+Deliberate differences from the reference, all on inputs it cannot serve:
+  * no LDS ceiling on max_seq_len (the decode kernel streams the softmax, so
+    the threadgroup-memory check of mlx_paged_attention.cpp:192-199 can never
+    fail);
+  * key_cache's last dimension must equal 16 / element size (the reference
+    kernel hard-codes it without checking, paged_attention_kernels.metal:80);
+  * reshape_and_cache validates shapes (the reference checks none,
+    mlx_cache.cpp:256-278) and also accepts the token-major MHATokenPool
+    buffers [num_slots, Hkv, D];
+  * ``paged_attention_v2`` adds split-K decode, absent from the reference.
+"""
+
+from __future__ import annotations
+
+import threading
+
+import torch
+
+from . import _lib
+
+_DTYPE_CODE = {torch.float32: _lib.PKV_F32, torch.float16: _lib.PKV_F16, torch.bfloat16: _lib.PKV_BF16}
+_ELEM_BYTES = {torch.float32: 4, torch.float16: 2, torch.bfloat16: 2}
+_HEAD_SIZES = (32, 64, 80, 96, 112, 120, 128, 192, 256)
+_BLOCK_SIZES = (8, 16, 32)
+
+
+def _tensor(x, allow_none: bool = False):
+    if x is None and allow_none:
+        return None
+    if not isinstance(x, torch.Tensor):
+        raise TypeError("Expected torch.Tensor")
+    return x
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DTYPE_CODE[t.dtype]
+    except KeyError:
+        raise ValueError("Unsupported dtype") from None
+
+
+def _on_gpu(op: str, *tensors) -> torch.device:
+    dev = tensors[0].device
+    for t in tensors:
+        if t is not None and (t.device.type != "cuda" or t.device != dev):
+            raise RuntimeError(f"{op} is GPU-only")
+    if dev.type != "cuda":
+        raise RuntimeError(f"{op} is GPU-only")
+    return dev
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _as_i32(t: torch.Tensor) -> torch.Tensor:
+    """32-bit index buffer (the kernels read int32; uint32 keeps its bits)."""
+    if t.dtype != torch.int32:
+        if t.dtype.is_floating_point or t.dtype == torch.bool:
+            raise ValueError("index tensors must have an integer dtype")
+        t = t.to(torch.int32)
+    return t.contiguous()
+
+
+# ---------------------------------------------------------------------------
+# Decode scratch and arrival counters, one pair per (device, stream).  The
+# scratch needs no initialisation.  The counters are zero-filled when the
+# buffer is (re)allocated, and every call leaves them zero, so calls ordered
+# on one stream can share them whatever their shapes.
+# ---------------------------------------------------------------------------
+_ws_lock = threading.Lock()
+_ws_cache: dict = {}
+
+
+def _decode_buffers(dev: torch.device, stream: int, scratch_bytes: int, counter_bytes: int):
+    key = (dev.index, stream)
+    with _ws_lock:
+        scratch, counters = _ws_cache.get(key, (None, None))
+        if scratch is None or scratch.numel() < scratch_bytes:
+            scratch = torch.empty(max(scratch_bytes, 1 << 16), dtype=torch.uint8, device=dev)
+        if counters is None or counters.numel() * 4 < counter_bytes:
+            counters = torch.zeros(max(counter_bytes // 4, 1 << 12), dtype=torch.int32, device=dev)
+        _ws_cache[key] = (scratch, counters)
+        return scratch, counters
+
+
+def _check_paged_attention(query, key_cache, value_cache, block_tables, context_lens,
+                           num_kv_heads, block_size, max_seq_len, alibi_slopes):
+    """Checks of mlx_paged_attention.cpp:156-188, same order and messages."""
+    if query.dim() != 3:
+        raise ValueError("query must have shape [num_seqs, num_heads, head_size]")
+    if key_cache.dim() != 5 or value_cache.dim() != 4:
+        raise ValueError("key_cache/value_cache must use paged attention layouts")
+    if block_tables.dim() != 2 or context_lens.dim() != 1:
+        raise ValueError("block_tables must be 2D and context_lens must be 1D")
+    if query.shape[0] != block_tables.shape[0] or query.shape[0] != context_lens.shape[0]:
+        raise ValueError("query, block_tables, and context_lens sequence counts differ")
+    if num_kv_heads <= 0 or query.shape[1] % num_kv_heads != 0:
+        raise ValueError("num_heads must be divisible by num_kv_heads")
+    if key_cache.shape[1] != num_kv_heads or value_cache.shape[1] != num_kv_heads:
+        raise ValueError("cache KV-head count does not match num_kv_heads")
+    if key_cache.shape[2] * key_cache.shape[4] != query.shape[2] or value_cache.shape[2] != query.shape[2]:
+        raise ValueError("cache head size does not match query head size")
+    if (key_cache.shape[0] != value_cache.shape[0] or key_cache.shape[3] != block_size
+            or value_cache.shape[3] != block_size):
+        raise ValueError("cache block dimensions do not match block_size")
+    if alibi_slopes is not None and (alibi_slopes.dim() != 1 or alibi_slopes.shape[0] != query.shape[1]):
+        raise ValueError("alibi_slopes must have shape [num_heads]")
+    if max_seq_len <= 0:
+        raise ValueError("max_seq_len must be positive")
+    if max_seq_len > block_tables.shape[1] * block_size:
+        raise ValueError("max_seq_len exceeds block table capacity")
+    if query.shape[2] not in _HEAD_SIZES or block_size not in _BLOCK_SIZES:
+        raise ValueError("Unsupported head_size/block_size for paged_attention")
+    # Checks the reference leaves to the kernel.
+    qc = _dtype_code(query)
+    cc = _dtype_code(key_cache)
+    if value_cache.dtype != key_cache.dtype:
+        raise ValueError("key_cache and value_cache dtypes differ")
+    if key_cache.shape[4] != 16 // _ELEM_BYTES[key_cache.dtype]:
+        raise ValueError("key_cache last dimension must be 16 / element size of the cache dtype")
+    if not (qc == cc and qc != _lib.PKV_F32) and not (qc == _lib.PKV_F32 and cc != _lib.PKV_F32):
+        raise ValueError(
+            f"Unsupported query/cache dtype pair for paged_attention: {query.dtype}/{key_cache.dtype}")
+    return qc, cc
+
+
+def _paged_attention(op, query, key_cache, value_cache, block_tables, context_lens, num_kv_heads,
+                     scale, block_size, max_seq_len, alibi_slopes, partition_size):
+    for t in (query, key_cache, value_cache, block_tables, context_lens):
+        _tensor(t)
+    _tensor(alibi_slopes, allow_none=True)
+    num_kv_heads, block_size, max_seq_len = int(num_kv_heads), int(block_size), int(max_seq_len)
+    qc, cc = _check_paged_attention(query, key_cache, value_cache, block_tables, context_lens,
+                                    num_kv_heads, block_size, max_seq_len, alibi_slopes)
+    dev = _on_gpu(op, query, key_cache, value_cache, block_tables, context_lens, alibi_slopes)
+    B, Hq, D = query.shape
+    if query.stride(2) != 1 or query.stride(1) != D or (query.stride(0) * _ELEM_BYTES[query.dtype]) % 16:
+        query = query.contiguous()
+    if key_cache.stride()[2:] != (block_size * key_cache.shape[4], key_cache.shape[4], 1):
+        key_cache = key_cache.contiguous()
+    if value_cache.stride()[2:] != (block_size, 1):
+        value_cache = value_cache.contiguous()
+    bt = _as_i32(block_tables)
+    lens = _as_i32(context_lens)
+    alibi = None if alibi_slopes is None else alibi_slopes.to(torch.float32).contiguous()
+    out = torch.empty((B, Hq, D), dtype=query.dtype, device=dev)
+    if B == 0:
+        return out
+    lib = _lib.lib()
+    with torch.cuda.device(dev):
+        stream = _stream(dev)
+        need = lib.pkv_paged_attention_workspace_size(B, Hq, num_kv_heads, D, max_seq_len,
+                                                      partition_size)
+        if need == 0:
+            _lib.check(_lib.PKV_ERR_INVALID)
+        ws, cnt = _decode_buffers(dev, stream, need, lib.pkv_paged_attention_counter_size(B, Hq, num_kv_heads))
+        st = lib.pkv_paged_attention(
+            out.data_ptr(), query.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
+            bt.data_ptr(), lens.data_ptr(), None if alibi is None else alibi.data_ptr(),
+            B, Hq, num_kv_heads, D, block_size, bt.shape[1], max_seq_len, key_cache.shape[0],
+            float(scale), query.stride(0), key_cache.stride(0), key_cache.stride(1),
+            value_cache.stride(0), value_cache.stride(1), _lib.PKV_LAYOUT_PAGED5D, partition_size,
+            ws.data_ptr(), ws.numel(), cnt.data_ptr(), cnt.numel() * 4, qc, cc, stream)
+    _lib.check(st)
+    return out
+
+
+def paged_attention_v1(query, key_cache, value_cache, block_tables, seq_lens, num_kv_heads,
+                       scale, block_size, max_seq_len, alibi_slopes=None):
+    """Single-softmax paged decode attention (bindings.cpp:44-65).
+
+    Returns a new tensor shaped and typed like ``query``
+    (mlx_paged_attention.cpp:212).
+    """
+    return _paged_attention("PagedAttentionV1", query, key_cache, value_cache, block_tables, seq_lens,
+                            num_kv_heads, scale, block_size, max_seq_len, alibi_slopes, 0)
+
+
+def paged_attention_v2(query, key_cache, value_cache, block_tables, seq_lens, num_kv_heads,
+                       scale, block_size, max_seq_len, alibi_slopes=None, partition_size=512):
+    """Split-K paged decode: softmax per partition of ``partition_size``
+    tokens, merged across partitions by log-sum-exp.  Same arguments and
+    result as ``paged_attention_v1`` plus ``partition_size``."""
+    partition_size = int(partition_size)
+    if partition_size <= 0 or partition_size % 16 or partition_size % int(block_size) or partition_size > 1024:
+        raise ValueError("partition_size must be a positive multiple of 16 and of block_size, at most 1024")
+    return _paged_attention("PagedAttentionV2", query, key_cache, value_cache, block_tables, seq_lens,
+                            num_kv_heads, scale, block_size, max_seq_len, alibi_slopes, partition_size)
+
+
+def _reshape_and_cache(op, key, value, key_cache, value_cache, slot_mapping, flash: bool):
+    for t in (key, value, key_cache, value_cache, slot_mapping):
+        _tensor(t)
+    if key.dim() != 3 or value.shape != key.shape:
+        raise ValueError("key and value must have shape [num_tokens, num_kv_heads, head_size]")
+    if slot_mapping.dim() != 1 or slot_mapping.shape[0] != key.shape[0]:
+        raise ValueError("slot_mapping must have shape [num_tokens]")
+    N, H, D = key.shape
+    if value_cache.dtype != key_cache.dtype:
+        raise ValueError("key_cache and value_cache dtypes differ")
+    kvc, cc = _dtype_code(key), _dtype_code(key_cache)
+    if value.dtype != key.dtype:
+        raise ValueError("key and value dtypes differ")
+    if not (kvc == cc or kvc == _lib.PKV_F32):
+        raise ValueError(f"Unsupported key/cache dtype pair: {key.dtype} -> {key_cache.dtype}")
+    x = 16 // _ELEM_BYTES[key_cache.dtype]
+    if not flash and key_cache.dim() == 5:
+        layout = _lib.PKV_LAYOUT_PAGED5D
+        nb, bs = key_cache.shape[0], key_cache.shape[3]
+        if tuple(key_cache.shape) != (nb, H, D // x, bs, x) or D % x:
+            raise ValueError("key_cache must have shape [num_blocks, num_kv_heads, head_size/x, block_size, x]")
+        if tuple(value_cache.shape) != (nb, H, D, bs):
+            raise ValueError("value_cache must have shape [num_blocks, num_kv_heads, head_size, block_size]")
+        num_slots = nb * bs
+    elif key_cache.dim() in ((3, 4) if flash else (3,)):
+        layout = _lib.PKV_LAYOUT_TOKEN_MAJOR
+        if tuple(key_cache.shape[-2:]) != (H, D) or value_cache.shape != key_cache.shape:
+            raise ValueError("token-major caches must have shape [..., num_kv_heads, head_size]")
+        num_slots = key_cache.numel() // (H * D) if H * D else 0
+        bs = key_cache.shape[1] if key_cache.dim() == 4 else 1
+    else:
+        raise ValueError("key_cache/value_cache must use a paged or token-major layout")
+    if not key_cache.is_contiguous() or not value_cache.is_contiguous():
+        raise ValueError("key_cache and value_cache must be contiguous (they are updated in place)")
+    dev = _on_gpu(op, key, value, key_cache, value_cache, slot_mapping)
+    if key.stride()[1:] != (D, 1):
+        key = key.contiguous()
+    if value.stride()[1:] != (D, 1):
+        value = value.contiguous()
+    slots = _as_i32(slot_mapping)
+    if N == 0:
+        return [key_cache, value_cache]
+    lib = _lib.lib()
+    with torch.cuda.device(dev):
+        st = lib.pkv_reshape_and_cache(
+            key.data_ptr(), value.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
+            slots.data_ptr(), N, H, D, key.stride(0), value.stride(0), layout, bs, x, num_slots,
+            kvc, cc, _stream(dev))
+    _lib.check(st)
+    return [key_cache, value_cache]
+
+
+def reshape_and_cache(key, value, key_cache, value_cache, slot_mapping):
+    """Scatter new tokens into the cache in place; returns [key_cache, value_cache].
+
+    Paged 5-D caches follow mlx_cache.cpp:256-278; 3-D [num_slots, Hkv, D]
+    caches (MHATokenPool buffers) use the token-major kernel.
+    """
+    return _reshape_and_cache("ReshapeAndCache", key, value, key_cache, value_cache, slot_mapping, False)
+
+
+def reshape_and_cache_flash(key, value, key_cache, value_cache, slot_mapping):
+    """Scatter into [num_blocks, block_size, Hkv, D] caches (mlx_cache.cpp:280-300)."""
+    return _reshape_and_cache("ReshapeAndCacheFlash", key, value, key_cache, value_cache, slot_mapping,
+                              True)
+
+
+def copy_blocks(key_caches, value_caches, block_mapping):
+    """Copy blocks src -> dst inside every cache (mlx_cache.cpp:302-346).
+
+    Not on the append/decode path; implemented with device tensor copies.
+    """
+    _tensor(block_mapping)
+    m = block_mapping.to(torch.int64).reshape(-1, 2)
+    for c in list(key_caches) + list(value_caches):
+        _tensor(c)
+        idx = m.to(c.device)
+        c[idx[:, 1]] = c[idx[:, 0]]
+    return list(key_caches), list(value_caches)
+
+
+def swap_blocks(src, dst, block_mapping):
+    """Copy blocks of ``src`` into ``dst`` (mlx_cache.cpp:348-370); returns dst.
+
+    Not on the append/decode path; implemented with tensor copies.
+    """
+    _tensor(src)
+    _tensor(dst)
+    _tensor(block_mapping)
+    m = block_mapping.to(torch.int64).reshape(-1, 2)
+    dst[m[:, 1].to(dst.device)] = src[m[:, 0].to(src.device)].to(dst.device)
+    return dst
+
+
+def get_device_attribute(attribute, device_id=0):
+    """hipDeviceGetAttribute(attribute, device_id)."""
+    import ctypes
+    v = ctypes.c_int64(0)
+    _lib.check(_lib.lib().pkv_get_device_attribute(int(attribute), int(device_id), ctypes.byref(v)))
+    return v.value
+
+
+def get_max_shared_memory_per_block_device_attribute(device_id=0):
+    """LDS bytes per workgroup (mlx_device.cpp:16-20)."""
+    import ctypes
+    v = ctypes.c_int64(0)
+    _lib.check(_lib.lib().pkv_max_shared_memory_per_block(int(device_id), ctypes.byref(v)))
+    return v.value
