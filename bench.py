@@ -1,0 +1,328 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X paged-KV hot path (one GPU).
+
+Default workload: one paged decode-attention layer at Llama-3-8B shape --
+64 sequences, 32 query heads over 8 KV heads (GQA 4), head_dim 128,
+block_size 16, context lengths uniform in [512, 4096], bf16 query and KV,
+block tables a seeded random permutation over a pool of 1.1x the blocks
+needed (block 0 is the padding block).  One step = one
+``paged_attention_v1`` call over the batch.  Independent per-layer KV pools
+(4 by default, 2.7 GB in all) are used in turn, as consecutive layers of a
+model would be, so neither L2 nor the 256 MiB Infinity Cache serves a step
+from the previous one.
+
+Printed: ONE JSON line with the driver's fields plus
+  roofline      the decode kernel's algorithmic HBM bytes per launch divided
+                by its mean launch time (HIP events around every launch, on
+                the stream the kernel runs on), against the 8 TB/s peak;
+                ``traffic`` is the measured HBM bytes per launch from the
+                committed rocprofv3 counter summary when present;
+  append        the slot-mapped append at 4096 tokens / 8 KV heads / D 128 /
+                bf16 into 65,536 slots with 5% padding, timed as a HIP graph
+                of back-to-back launches over rotating sources and pools, for
+                the token-major (MHATokenPool) and paged 5-D layouts;
+  cpu_baseline  the reference's gather + SDPA decode restated in torch on
+                this host's cores, on the same inputs (full batch, one layer).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import re
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "sglang-mlx_amd"))
+
+METRIC = "paged decode µs/step + HBM GB/s (% peak), bs64 ctx≤4k Llama-3-8B shape"
+PEAK_GBS = 8000.0  # MI355X HBM3E, published peak
+DECODE_KERNEL = "paged_decode_kernel<BF16, BF16, 128, 16>"
+APPEND_KERNEL = "rac_token_major_kernel<BF16, BF16, 8, true>"
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--layers", type=int, default=4, help="independent KV pools used in turn")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-append", action="store_true", help="skip the append measurement")
+    ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of timed CPU baseline work")
+    return ap.parse_args()
+
+
+# ---------------------------------------------------------------------------
+# Inputs
+# ---------------------------------------------------------------------------
+
+
+def decode_inputs(seed: int, B: int, Hq: int, Hkv: int, D: int, bs: int, ctx_lo: int, ctx_hi: int,
+                  layers: int, dev):
+    """Seeded decode-layer inputs generated on the device."""
+    rng = np.random.default_rng(seed)
+    ctx = rng.integers(ctx_lo, ctx_hi + 1, size=B).astype(np.int64)
+    nblk = -(-ctx // bs)
+    need = int(nblk.sum())
+    nb = int(math.ceil(need * 1.1)) + 1
+    perm = rng.permutation(np.arange(1, nb))
+    max_blocks = -(-ctx_hi // bs)
+    bt = np.full((B, max_blocks), -1, dtype=np.int32)
+    pos = 0
+    for s in range(B):
+        bt[s, :nblk[s]] = perm[pos:pos + nblk[s]]
+        pos += nblk[s]
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    q = torch.randn((B, Hq, D), generator=g, device=dev).to(torch.bfloat16)
+    pools = []
+    for _ in range(layers):
+        kc = torch.randn((nb, Hkv, D // 8, bs, 8), generator=g, device=dev).to(torch.bfloat16)
+        vc = torch.randn((nb, Hkv, D, bs), generator=g, device=dev).to(torch.bfloat16)
+        pools.append((kc, vc))
+    return dict(q=q, pools=pools, bt=torch.from_numpy(bt).to(dev), ctx=torch.from_numpy(ctx.astype(np.int32)).to(dev),
+                ctx_np=ctx, nb=nb, B=B, Hq=Hq, Hkv=Hkv, D=D, bs=bs, max_seq_len=ctx_hi)
+
+
+def decode_bytes(ctx: np.ndarray, B: int, Hq: int, Hkv: int, D: int, bs: int, s_kv=2, s_q=2, s_o=2) -> int:
+    """Algorithmic HBM bytes of one decode launch: every context token's K and
+    V read once per KV head, the queries read and outputs written once, the
+    used block-table entries and context lengths read once."""
+    return int(ctx.sum() * Hkv * D * 2 * s_kv + B * Hq * D * (s_q + s_o) + (-(-ctx // bs)).sum() * 4 + B * 4)
+
+
+# ---------------------------------------------------------------------------
+# Timing helpers
+# ---------------------------------------------------------------------------
+
+
+def timed_launches(fn, steps: int, warmup: int):
+    """Run fn(i) warmup times, then steps times with a HIP event pair around
+    each launch (current stream).  Returns (wall seconds, per-launch ms list)."""
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record()
+        fn(i)
+        ends[i].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return wall, [s.elapsed_time(e) for s, e in zip(starts, ends)]
+
+
+def graph_launch_ms(fn, launches: int, replays: int = 5):
+    """Mean device time of one launch: capture `launches` calls fn(i) in one
+    HIP graph, replay it and divide the event-timed replay by `launches`."""
+    for i in range(3):
+        fn(i)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(launches):
+            fn(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    per = []
+    for _ in range(replays):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        graph.replay()
+        b.record()
+        torch.cuda.synchronize()
+        per.append(a.elapsed_time(b) / launches)
+    per.sort()
+    return per[len(per) // 2]
+
+
+def read_traffic(name: str):
+    """HBM bytes per launch from a committed rocprofv3 counter summary
+    (profiles/<name>: a line 'traffic_bytes_per_launch: <int>'), else None."""
+    path = os.path.join(ROOT, "profiles", name)
+    try:
+        with open(path) as f:
+            for line in f:
+                m = re.match(r"\s*traffic_bytes_per_launch:\s*([0-9.eE+]+)", line)
+                if m:
+                    return int(float(m.group(1)))
+    except OSError:
+        pass
+    return None
+
+
+# ---------------------------------------------------------------------------
+# Legs
+# ---------------------------------------------------------------------------
+
+
+def bench_decode(args, dev, kernels):
+    inp = decode_inputs(1003, B=64, Hq=32, Hkv=8, D=128, bs=16, ctx_lo=512, ctx_hi=4096,
+                        layers=args.layers, dev=dev)
+    B, Hq, Hkv, D, bs = inp["B"], inp["Hq"], inp["Hkv"], inp["D"], inp["bs"]
+    scale = 1.0 / math.sqrt(D)
+    outs = [None] * len(inp["pools"])
+
+    def step(i):
+        li = i % len(inp["pools"])
+        kc, vc = inp["pools"][li]
+        outs[li] = kernels.paged_attention_v1(inp["q"], kc, vc, inp["bt"], inp["ctx"], Hkv, scale, bs,
+                                              inp["max_seq_len"])
+
+    wall, per = timed_launches(step, args.steps, args.warmup)
+    nbytes = decode_bytes(inp["ctx_np"], B, Hq, Hkv, D, bs)
+    ms_step = wall * 1e3 / args.steps
+    per_sorted = sorted(per)
+    mean_ms = sum(per) / len(per)
+    achieved = nbytes / (mean_ms * 1e-3) / 1e9
+    res = dict(inp=inp, scale=scale, out0=outs[0], nbytes=nbytes, ms_step=ms_step, mean_ms=mean_ms,
+               median_ms=per_sorted[len(per) // 2], achieved=achieved)
+    return res
+
+
+def bench_append(dev, kernels, sources: int = 24, pools: int = 4, launches: int = 96):
+    """Append workload: 4096 tokens, 8 KV heads, D 128, bf16, 65,536 slots
+    (4096 blocks of 16), unique random slots (slot 0 reserved), 5% = -1."""
+    N, H, D, S, bs = 4096, 8, 128, 65536, 16
+    rng = np.random.default_rng(1002)
+    g = torch.Generator(device=dev)
+    g.manual_seed(1002)
+    srcs, maps, nvalid = [], [], []
+    for _ in range(sources):
+        slots = rng.choice(S - 1, size=N, replace=False).astype(np.int64) + 1
+        slots[rng.choice(N, size=int(round(0.05 * N)), replace=False)] = -1
+        nvalid.append(int((slots >= 0).sum()))
+        maps.append(torch.from_numpy(slots.astype(np.int32)).to(dev))
+        srcs.append((torch.randn((N, H, D), generator=g, device=dev).to(torch.bfloat16),
+                     torch.randn((N, H, D), generator=g, device=dev).to(torch.bfloat16)))
+    nv = sum(nvalid) / len(nvalid)
+    nbytes = int(2 * nv * H * D * 2 + 2 * nv * H * D * 2 + N * 4)
+    out = {}
+    for layout in ("token_major", "paged5d"):
+        if layout == "token_major":
+            caches = [(torch.zeros((S, H, D), dtype=torch.bfloat16, device=dev),
+                       torch.zeros((S, H, D), dtype=torch.bfloat16, device=dev)) for _ in range(pools)]
+        else:
+            caches = [(torch.zeros((S // bs, H, D // 8, bs, 8), dtype=torch.bfloat16, device=dev),
+                       torch.zeros((S // bs, H, D, bs), dtype=torch.bfloat16, device=dev)) for _ in range(pools)]
+
+        def launch(i):
+            k, v = srcs[i % sources]
+            kc, vc = caches[i % pools]
+            kernels.reshape_and_cache(k, v, kc, vc, maps[i % sources])
+
+        ms = graph_launch_ms(launch, launches)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[layout] = dict(us_per_launch=round(ms * 1e3, 3), achieved_gbs=round(gbs, 1),
+                           frac=round(gbs / PEAK_GBS, 4))
+        del caches
+    torch.cuda.synchronize()
+    out["bytes_per_launch"] = nbytes
+    out["workload"] = ("reshape_and_cache: 4096 tokens, 8 kv heads, D128, bf16, 65536 slots "
+                       "(4096 blocks of 16), unique random slots, 5% padding")
+    out["kernel"] = APPEND_KERNEL
+    out["method"] = f"HIP graph of {launches} launches over {sources} sources x {pools} pools, median of 5 replays"
+    return out
+
+
+def bench_cpu(res, budget_s):
+    """CPU baseline leg: the oracle package's torch-CPU gather + SDPA, same
+    inputs (layer 0), full batch."""
+    from oracle import cpu_baseline as cb
+
+    inp = res["inp"]
+    kc, vc = inp["pools"][0]
+    nb, Hkv, D, bs = inp["nb"], inp["Hkv"], inp["D"], inp["bs"]
+    # Token-major pool [nb*bs, Hkv, D], as MHATokenPool stores it (slot = block*bs + offset).
+    k_pool = kc.permute(0, 3, 1, 2, 4).reshape(nb * bs, Hkv, D).cpu()
+    v_pool = vc.permute(0, 3, 1, 2).reshape(nb * bs, Hkv, D).cpu()
+    q, bt, ctx = inp["q"].cpu(), inp["bt"].cpu(), inp["ctx"].cpu()
+    t = cb.time_decode(q, k_pool, v_pool, bt, ctx, bs, res["scale"], budget_s=budget_s)
+    cpu_out = cb.gather_sdpa_decode(q, k_pool, v_pool, bt, ctx, bs, res["scale"])
+    diff = (cpu_out.float() - res["out0"].float().cpu()).abs().max().item()
+    gbs = res["nbytes"] / t["median_s"] / 1e9
+    return dict(value=round(gbs, 2), unit="GB/s", cores=t["threads"], kind="port",
+                sample=(f"full batch (64 seqs, one layer), gather+SDPA per sequence in torch-CPU bf16, "
+                        f"median of {t['iters']} iterations"),
+                us_per_step=round(t["median_s"] * 1e6, 1), cpu=t["cpu"],
+                label="CPU restatement of the reference's gather+SDPA path (MLX CPU backend unavailable offline)",
+                max_abs_diff_vs_gpu=round(diff, 5))
+
+
+def main():
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU: --gpus {args.gpus} (WORLD_SIZE={world}) is not supported; "
+              "the paged-KV path is benchmarked on a single MI355X", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        sys.exit(1)
+    from sglang_mlx_amd import kernels
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    res = bench_decode(args, dev, kernels)
+    inp = res["inp"]
+    B = inp["B"]
+    us = res["ms_step"] * 1e3
+    value = res["nbytes"] / (res["ms_step"] * 1e-3) / 1e9
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(res["ms_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "llama3-8b paged decode layer: B64, 32 q / 8 kv heads, D128, bs16, ctx U[512,4096], bf16",
+            "batch": B, "num_heads": inp["Hq"], "num_kv_heads": inp["Hkv"], "head_size": inp["D"],
+            "block_size": inp["bs"], "ctx_range": [512, 4096], "mean_ctx": float(inp["ctx_np"].mean()),
+            "num_blocks": inp["nb"], "kv_pools_rotated": len(inp["pools"]), "parallelism": "none (1 GPU)",
+        },
+        "us_per_step": round(us, 2),
+        "tokens_per_s": round(B / (res["ms_step"] * 1e-3), 1),
+        "hbm_frac": round(value / PEAK_GBS, 4),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(res["achieved"], 1),
+            "peak": PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(res["achieved"] / PEAK_GBS, 4),
+            "traffic": read_traffic("paged_decode_llama3_8b_traffic.txt"),
+            "kernel": DECODE_KERNEL,
+            "bytes_per_launch": res["nbytes"],
+            "mean_launch_us": round(res["mean_ms"] * 1e3, 2),
+            "median_launch_us": round(res["median_ms"] * 1e3, 2),
+        },
+    }
+    if not args.no_append:
+        line["append"] = bench_append(dev, kernels)
+    if not args.no_cpu:
+        line["cpu_baseline"] = bench_cpu(res, args.cpu_budget)
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

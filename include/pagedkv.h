@@ -92,25 +92,16 @@ int pkv_reshape_and_cache(const void* key, const void* value,
  * Scratch bytes that pkv_paged_attention needs for these sizes (per-partition
  * (max, sum) pairs and per-partition outputs, float32).  partition_size = 0
  * selects the single-pass (v1) semantics; the library then chooses its own
- * internal split.  The scratch needs no initialisation.  Returns 0 for
- * invalid sizes.
+ * internal split.  The scratch needs no initialisation and is only read by
+ * the launch that wrote it, so calls ordered on one stream may share one
+ * buffer; calls that overlap in time must not.  Returns 0 for invalid
+ * sizes.
  */
 size_t pkv_paged_attention_workspace_size(int32_t num_seqs, int32_t num_heads,
                                           int32_t num_kv_heads,
                                           int32_t head_size,
                                           int32_t max_seq_len,
                                           int32_t partition_size);
-
-/*
- * Bytes of arrival counters (one small int32 array per sequence and head
- * group) that pkv_paged_attention needs.  The counter buffer must be all
- * zero the first time it is used; every call leaves it all zero again, so one
- * zero-filled buffer (of the largest size needed) serves any number of calls
- * ordered on one stream.  Calls that overlap in time must not share it.
- * Returns 0 for invalid sizes.
- */
-size_t pkv_paged_attention_counter_size(int32_t num_seqs, int32_t num_heads,
-                                        int32_t num_kv_heads);
 
 /*
  * Block-table decode attention.
@@ -126,6 +117,8 @@ size_t pkv_paged_attention_counter_size(int32_t num_seqs, int32_t num_heads,
  * partition_size > 0 : split-K (paged_attention_v2): partitions of
  *                      partition_size tokens, merged by log-sum-exp.  Must be
  *                      a multiple of 16 and of block_size, at most 1024.
+ * Launches: one partition kernel, plus a log-sum-exp merge kernel when the
+ * call has more than one partition per sequence; both on `stream`.
  * query   : [num_seqs, num_heads, head_size], row stride q_stride.
  * out     : [num_seqs, num_heads, head_size] contiguous, same dtype as query.
  * block_tables: [num_seqs, max_num_blocks_per_seq]; entries past
@@ -151,7 +144,6 @@ int pkv_paged_attention(void* out, const void* query, const void* key_cache,
                         int64_t v_block_stride, int64_t v_head_stride,
                         int32_t layout, int32_t partition_size,
                         void* workspace, size_t workspace_bytes,
-                        int32_t* counters, size_t counter_bytes,
                         int32_t q_dtype, int32_t cache_dtype, void* stream);
 
 /*

@@ -1,0 +1,110 @@
+"""CPU baseline: torch-CPU restatement of the reference's gather + SDPA decode.
+
+TEST INFRASTRUCTURE ONLY -- used by the ``cpu_baseline`` leg of bench.py
+(and by the CPU tests that check it against the float64 oracle).  Nothing in
+the product package imports it.
+
+The reference decodes without its paged kernel: each layer scatters the new
+token into the token-major MHATokenPool buffers, gathers every token of the
+sequence back into a contiguous [1, Hkv, T, D] copy
+(sglang_mlx/srt/mem_cache/memory_pool.py:139-159, called from
+PooledKVCache.update_and_fetch, :206-234) and hands that copy to MLX's
+scaled_dot_product_attention, one sequence at a time (the runner's batch is
+1, sglang_mlx/model_runner.py:278).  tests/bench_paged_vs_gather.py:81-103
+times the same gather + SDPA.  MLX is not installed (and has no ROCm
+backend), so this restatement runs the same steps with torch on the host:
+
+  1. slots of logical token t: block_table[t // bs] * bs + t % bs
+     (token-major pool, slot = block * bs + offset);
+  2. index_select those rows of the [num_slots, Hkv, D] K and V buffers,
+     transpose to [1, Hkv, T, D];
+  3. torch.nn.functional.scaled_dot_product_attention(q[1, Hq, 1, D], k, v,
+     scale, enable_gqa=True).
+
+The 1e-6 in the reference kernel's softmax denominator is a kernel detail
+(paged_attention_kernels.metal:144), absent from SDPA, so results differ
+from the oracle by a relative 1e-6 plus SDPA's own rounding.
+"""
+
+from __future__ import annotations
+
+import os
+import time
+
+import torch
+import torch.nn.functional as F
+
+
+def host_threads() -> int:
+    """Threads the baseline may use: the process's CPU affinity, capped by
+    OMP_NUM_THREADS when that is set (the GPU box sets it to its CPU share)."""
+    n = len(os.sched_getaffinity(0))
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit() and int(env) > 0:
+        n = min(n, int(env))
+    return max(1, n)
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def token_slots(block_row: torch.Tensor, ctx: int, block_size: int) -> torch.Tensor:
+    """Pool slots of logical tokens 0..ctx-1 (int64)."""
+    t = torch.arange(ctx, dtype=torch.int64)
+    return block_row.to(torch.int64)[t // block_size] * block_size + t % block_size
+
+
+def gather_sdpa_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                       block_tables: torch.Tensor, context_lens: torch.Tensor, block_size: int,
+                       scale: float, seqs=None) -> torch.Tensor:
+    """One decode layer, sequence by sequence, on CPU tensors.
+
+    q [B, Hq, D]; k_pool / v_pool [num_slots, Hkv, D] (token-major);
+    block_tables [B, max_blocks]; context_lens [B].  Returns [B, Hq, D] in
+    q's dtype (rows of sequences outside ``seqs`` or with ctx 0 are zero).
+    """
+    B, Hq, D = q.shape
+    out = torch.zeros_like(q)
+    for s in (range(B) if seqs is None else seqs):
+        ctx = int(context_lens[s])
+        if ctx <= 0:
+            continue
+        idx = token_slots(block_tables[s], ctx, block_size)
+        k = k_pool.index_select(0, idx).transpose(0, 1).unsqueeze(0)  # [1, Hkv, T, D]
+        v = v_pool.index_select(0, idx).transpose(0, 1).unsqueeze(0)
+        o = F.scaled_dot_product_attention(q[s].reshape(1, Hq, 1, D), k, v, scale=scale,
+                                           enable_gqa=True)
+        out[s] = o.reshape(Hq, D)
+    return out
+
+
+def time_decode(q, k_pool, v_pool, block_tables, context_lens, block_size, scale,
+                budget_s: float = 10.0, min_iters: int = 5, seqs=None) -> dict:
+    """Median wall time of gather_sdpa_decode over >= min_iters runs (after
+    one warm-up), stopping once ``budget_s`` of timed work is done."""
+    threads = host_threads()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        gather_sdpa_decode(q, k_pool, v_pool, block_tables, context_lens, block_size, scale, seqs)
+        times = []
+        t_all = time.perf_counter()
+        while len(times) < min_iters or time.perf_counter() - t_all < budget_s:
+            t0 = time.perf_counter()
+            gather_sdpa_decode(q, k_pool, v_pool, block_tables, context_lens, block_size, scale, seqs)
+            times.append(time.perf_counter() - t0)
+            if len(times) >= 1000:
+                break
+        times.sort()
+        return dict(median_s=times[len(times) // 2], iters=len(times), threads=threads,
+                    cpu=cpu_model())
+    finally:
+        torch.set_num_threads(prev)

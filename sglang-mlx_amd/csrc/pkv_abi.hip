@@ -66,7 +66,11 @@ int resolve_partition(int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
   }
   const int64_t parts = ceil_div(max_seq_len, ps);
   if (parts > pkv::kMaxParts)
-    return fail(PKV_ERR_UNSUPPORTED, "max_seq_len / partition_size exceeds 1024 partitions");
+    return fail(PKV_ERR_UNSUPPORTED, "max_seq_len / partition_size exceeds 65536 partitions");
+  // One 256-thread workgroup per (partition, sequence, unit); HIP bounds a
+  // launch to 2^32 work-items.
+  if (parts * num_seqs * units * 256 >= ((int64_t)1 << 32))
+    return fail(PKV_ERR_UNSUPPORTED, "num_seqs * num_kv_heads * partitions exceeds the launch grid limit");
   *ps_out = ps;
   *parts_out = (int32_t)parts;
   return PKV_OK;
@@ -83,11 +87,6 @@ DecodeWorkspace decode_workspace_layout(int32_t num_seqs, int32_t num_heads, int
   w.o_bytes = align((size_t)num_seqs * num_heads * max_parts * head_size * sizeof(float));
   w.total = w.ml_bytes + w.o_bytes;
   return w;
-}
-size_t decode_counter_bytes(int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads) {
-  const int32_t group = num_heads / num_kv_heads;
-  const int32_t units = num_kv_heads * ((group + 15) / 16);
-  return (size_t)num_seqs * units * (1 + kMaxGroups) * sizeof(int32_t);
 }
 }  // namespace pkv
 
@@ -157,19 +156,14 @@ size_t pkv_paged_attention_workspace_size(int32_t num_seqs, int32_t num_heads, i
   return pkv::decode_workspace_layout(num_seqs, num_heads, head_size, parts).total;
 }
 
-size_t pkv_paged_attention_counter_size(int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads) {
-  if (num_seqs < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0) return 0;
-  return pkv::decode_counter_bytes(num_seqs, num_heads, num_kv_heads);
-}
-
 int pkv_paged_attention(void* out, const void* query, const void* key_cache, const void* value_cache,
                         const int32_t* block_tables, const int32_t* context_lens, const float* alibi_slopes,
                         int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads, int32_t head_size,
                         int32_t block_size, int32_t max_num_blocks_per_seq, int32_t max_seq_len,
                         int64_t num_blocks, float scale, int64_t q_stride, int64_t k_block_stride,
                         int64_t k_head_stride, int64_t v_block_stride, int64_t v_head_stride, int32_t layout,
-                        int32_t partition_size, void* workspace, size_t workspace_bytes, int32_t* counters,
-                        size_t counter_bytes, int32_t q_dtype, int32_t cache_dtype, void* stream) {
+                        int32_t partition_size, void* workspace, size_t workspace_bytes, int32_t q_dtype,
+                        int32_t cache_dtype, void* stream) {
   if (num_seqs < 0) return fail(PKV_ERR_INVALID, "num_seqs must be non-negative");
   int32_t ps = 0, parts = 0;
   const int st = resolve_partition(num_seqs, num_heads, num_kv_heads, max_seq_len, block_size, partition_size,
@@ -200,10 +194,7 @@ int pkv_paged_attention(void* out, const void* query, const void* key_cache, con
   if (parts > 1) {
     if (workspace == nullptr || workspace_bytes < w.total)
       return fail(PKV_ERR_INVALID, "workspace is smaller than pkv_paged_attention_workspace_size()");
-    if (counters == nullptr || counter_bytes < pkv::decode_counter_bytes(num_seqs, num_heads, num_kv_heads))
-      return fail(PKV_ERR_INVALID, "counter buffer is smaller than pkv_paged_attention_counter_size()");
-    if (!aligned16(workspace) || !aligned16(counters))
-      return fail(PKV_ERR_INVALID, "workspace and counters must be 16-byte aligned");
+    if (!aligned16(workspace)) return fail(PKV_ERR_INVALID, "workspace must be 16-byte aligned");
   }
 
   pkv::DecodeParams p;
@@ -215,7 +206,6 @@ int pkv_paged_attention(void* out, const void* query, const void* key_cache, con
   p.block_tables = block_tables;
   p.context_lens = context_lens;
   p.alibi = alibi_slopes;
-  p.ws_count = counters;
   p.ws_ml = ws ? reinterpret_cast<float*>(ws) : nullptr;
   p.ws_o = ws ? reinterpret_cast<float*>(ws + w.ml_bytes) : nullptr;
   p.num_blocks = num_blocks;

@@ -11,14 +11,11 @@ namespace pkv {
 
 enum { kF32 = 0, kF16 = 1, kBF16 = 2 };
 
-// Largest split-K partition and the tile height of the decode kernel.
+// Largest split-K partition, the tile height of the decode kernel, and the
+// most partitions one sequence may be split into.
 constexpr int kMaxPartition = 1024;
 constexpr int kTile = 16;
-// Partitions merged per first-level group, and the second-level fan-in;
-// together they bound the partitions of one sequence to 16 * 64 = 1024.
-constexpr int kGroup = 16;
-constexpr int kMaxGroups = 64;
-constexpr int kMaxParts = kGroup * kMaxGroups;
+constexpr int kMaxParts = 65536;
 
 struct RacParams {
   const void* key;
@@ -50,7 +47,6 @@ struct DecodeParams {
   const float* alibi;         // [Hq] or null
   float* ws_ml;               // [B, Hq, max_parts, 2]: (max, sum) per partition, log2 domain
   float* ws_o;                // [B, Hq, max_parts, D]: normalised partition outputs
-  int32_t* ws_count;          // [B, units, 1 + kMaxGroups]: arrival counters, zero between calls
   int64_t num_blocks;
   int64_t q_stride;
   int64_t k_block_stride, k_head_stride;
@@ -68,14 +64,12 @@ struct DecodeParams {
   int32_t max_parts;          // ceil(max_seq_len / partition)
 };
 
-// Scratch carve-up shared by the size query and the launcher.  The arrival
-// counters live in a separate, caller-zeroed buffer of decode_counter_bytes().
+// Scratch carve-up shared by the size query and the launcher.
 struct DecodeWorkspace {
   size_t ml_bytes, o_bytes, total;
 };
 DecodeWorkspace decode_workspace_layout(int32_t num_seqs, int32_t num_heads, int32_t head_size,
                                         int32_t max_parts);
-size_t decode_counter_bytes(int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads);
 
 struct F32;
 struct F16;

@@ -72,25 +72,22 @@ def _as_i32(t: torch.Tensor) -> torch.Tensor:
 
 
 # ---------------------------------------------------------------------------
-# Decode scratch and arrival counters, one pair per (device, stream).  The
-# scratch needs no initialisation.  The counters are zero-filled when the
-# buffer is (re)allocated, and every call leaves them zero, so calls ordered
-# on one stream can share them whatever their shapes.
+# Decode scratch, one buffer per (device, stream).  It needs no
+# initialisation and each launch reads only what it wrote, so calls ordered
+# on one stream share it whatever their shapes.
 # ---------------------------------------------------------------------------
 _ws_lock = threading.Lock()
 _ws_cache: dict = {}
 
 
-def _decode_buffers(dev: torch.device, stream: int, scratch_bytes: int, counter_bytes: int):
+def _decode_scratch(dev: torch.device, stream: int, scratch_bytes: int) -> torch.Tensor:
     key = (dev.index, stream)
     with _ws_lock:
-        scratch, counters = _ws_cache.get(key, (None, None))
+        scratch = _ws_cache.get(key)
         if scratch is None or scratch.numel() < scratch_bytes:
             scratch = torch.empty(max(scratch_bytes, 1 << 16), dtype=torch.uint8, device=dev)
-        if counters is None or counters.numel() * 4 < counter_bytes:
-            counters = torch.zeros(max(counter_bytes // 4, 1 << 12), dtype=torch.int32, device=dev)
-        _ws_cache[key] = (scratch, counters)
-        return scratch, counters
+            _ws_cache[key] = scratch
+        return scratch
 
 
 def _check_paged_attention(query, key_cache, value_cache, block_tables, context_lens,
@@ -163,14 +160,14 @@ def _paged_attention(op, query, key_cache, value_cache, block_tables, context_le
                                                       partition_size)
         if need == 0:
             _lib.check(_lib.PKV_ERR_INVALID)
-        ws, cnt = _decode_buffers(dev, stream, need, lib.pkv_paged_attention_counter_size(B, Hq, num_kv_heads))
+        ws = _decode_scratch(dev, stream, need)
         st = lib.pkv_paged_attention(
             out.data_ptr(), query.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
             bt.data_ptr(), lens.data_ptr(), None if alibi is None else alibi.data_ptr(),
             B, Hq, num_kv_heads, D, block_size, bt.shape[1], max_seq_len, key_cache.shape[0],
             float(scale), query.stride(0), key_cache.stride(0), key_cache.stride(1),
             value_cache.stride(0), value_cache.stride(1), _lib.PKV_LAYOUT_PAGED5D, partition_size,
-            ws.data_ptr(), ws.numel(), cnt.data_ptr(), cnt.numel() * 4, qc, cc, stream)
+            ws.data_ptr(), ws.numel(), qc, cc, stream)
     _lib.check(st)
     return out
 

@@ -41,7 +41,6 @@ SIGNATURES = {
         _c_void_p,                                                 # stream
     ]),
     "pkv_paged_attention_workspace_size": (_size, [_i32, _i32, _i32, _i32, _i32, _i32]),
-    "pkv_paged_attention_counter_size": (_size, [_i32, _i32, _i32]),
     "pkv_paged_attention": (ctypes.c_int, [
         _c_void_p, _c_void_p, _c_void_p, _c_void_p,              # out, q, kc, vc
         _c_void_p, _c_void_p, _c_void_p,                          # block_tables, ctx, alibi
@@ -51,7 +50,6 @@ SIGNATURES = {
         _i64, _i64, _i64, _i64,                                   # k/v block & head strides
         _i32, _i32,                                               # layout, partition_size
         _c_void_p, _size,                                         # workspace, bytes
-        _c_void_p, _size,                                         # counters, bytes
         _i32, _i32, _c_void_p,                                    # q dtype, cache dtype, stream
     ]),
     "pkv_max_shared_memory_per_block": (ctypes.c_int, [_i32, ctypes.POINTER(_i64)]),
