@@ -45,7 +45,7 @@ sys.path.insert(0, os.path.join(ROOT, "sglang-mlx_amd"))
 
 METRIC = "paged decode µs/step + HBM GB/s (% peak), bs64 ctx≤4k Llama-3-8B shape"
 PEAK_GBS = 8000.0  # MI355X HBM3E, published peak
-DECODE_KERNEL = "paged_decode_kernel<BF16, BF16, 128, 16>"
+DECODE_KERNEL = "paged_decode_part_kernel<BF16, BF16, 128, 16> + paged_decode_reduce_kernel<BF16, 128>"
 APPEND_KERNEL = "rac_token_major_kernel<BF16, BF16, 8, true>"
 
 
@@ -58,6 +58,10 @@ def parse_args():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-append", action="store_true", help="skip the append measurement")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of timed CPU baseline work")
+    ap.add_argument("--only", choices=["decode", "append", "copy"],
+                    help="run one leg and print its own short JSON line (for counter collection under "
+                         "rocprofv3 --pmc): the decode layer, the token-major append, or a plain 1 GiB device "
+                         "copy whose FETCH_SIZE / WRITE_SIZE calibrate the counters")
     return ap.parse_args()
 
 
@@ -261,6 +265,26 @@ def bench_cpu(res, budget_s):
                 max_abs_diff_vs_gpu=round(diff, 5))
 
 
+def only_leg(args, dev, kernels):
+    """One leg alone, for rocprofv3 counter runs."""
+    if args.only == "decode":
+        res = bench_decode(args, dev, kernels)
+        print(json.dumps(dict(leg="decode", kernel=DECODE_KERNEL, bytes_per_launch=res["nbytes"],
+                              mean_launch_us=round(res["mean_ms"] * 1e3, 2), launches=args.steps + args.warmup)))
+    elif args.only == "append":
+        out = bench_append(dev, kernels)
+        print(json.dumps(dict(leg="append", **out)))
+    else:
+        n = 1 << 30
+        src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps(dict(leg="copy", bytes_read_per_launch=n, bytes_written_per_launch=n,
+                              launches=args.steps)))
+
+
 def main():
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -275,6 +299,9 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.only:
+        only_leg(args, dev, kernels)
+        return
     res = bench_decode(args, dev, kernels)
     inp = res["inp"]
     B = inp["B"]

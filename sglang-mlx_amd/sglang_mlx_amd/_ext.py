@@ -62,11 +62,15 @@ def _stream(dev: torch.device) -> int:
     return torch.cuda.current_stream(dev).cuda_stream
 
 
+def _check_index(t: torch.Tensor) -> None:
+    if t.dtype.is_floating_point or t.dtype.is_complex or t.dtype == torch.bool:
+        raise ValueError("index tensors must have an integer dtype")
+
+
 def _as_i32(t: torch.Tensor) -> torch.Tensor:
     """32-bit index buffer (the kernels read int32; uint32 keeps its bits)."""
+    _check_index(t)
     if t.dtype != torch.int32:
-        if t.dtype.is_floating_point or t.dtype == torch.bool:
-            raise ValueError("index tensors must have an integer dtype")
         t = t.to(torch.int32)
     return t.contiguous()
 
@@ -139,6 +143,8 @@ def _paged_attention(op, query, key_cache, value_cache, block_tables, context_le
     num_kv_heads, block_size, max_seq_len = int(num_kv_heads), int(block_size), int(max_seq_len)
     qc, cc = _check_paged_attention(query, key_cache, value_cache, block_tables, context_lens,
                                     num_kv_heads, block_size, max_seq_len, alibi_slopes)
+    _check_index(block_tables)
+    _check_index(context_lens)
     dev = _on_gpu(op, query, key_cache, value_cache, block_tables, context_lens, alibi_slopes)
     B, Hq, D = query.shape
     if query.stride(2) != 1 or query.stride(1) != D or (query.stride(0) * _ELEM_BYTES[query.dtype]) % 16:
@@ -229,6 +235,7 @@ def _reshape_and_cache(op, key, value, key_cache, value_cache, slot_mapping, fla
         raise ValueError("key_cache/value_cache must use a paged or token-major layout")
     if not key_cache.is_contiguous() or not value_cache.is_contiguous():
         raise ValueError("key_cache and value_cache must be contiguous (they are updated in place)")
+    _check_index(slot_mapping)
     dev = _on_gpu(op, key, value, key_cache, value_cache, slot_mapping)
     if key.stride()[1:] != (D, 1):
         key = key.contiguous()

@@ -1,0 +1,141 @@
+"""The C-ABI library: it loads, exports every entry point that
+include/pagedkv.h declares with the argument count the ctypes table uses,
+and rejects bad arguments with the documented status codes and messages
+before any HIP call.  No kernel is launched (no call here reaches a launch),
+so this runs without a GPU.
+"""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from sglang_mlx_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "pagedkv.h")
+
+
+def header_functions():
+    """name -> parameter count of every function declared in the header."""
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for m in re.finditer(r"(?:const\s+char\s*\*|int|size_t)\s+(pkv_\w+)\s*\(([^)]*)\)\s*;", text, flags=re.S):
+        params = m.group(2).strip()
+        out[m.group(1)] = 0 if params in ("", "void") else len(params.split(","))
+    return out
+
+
+def test_library_is_built_and_loads():
+    assert os.path.exists(_lib.LIB_PATH), "run __graft_entry__.build() first"
+    lib = _lib.lib()
+    assert b"gfx950" in lib.pkv_version()
+
+
+def test_every_declared_symbol_is_exported_with_matching_arity():
+    decl = header_functions()
+    assert set(decl) == set(_lib.SIGNATURES), (set(decl) ^ set(_lib.SIGNATURES))
+    handle = ctypes.CDLL(_lib.LIB_PATH)
+    for name, nparams in decl.items():
+        getattr(handle, name)  # AttributeError if not exported
+        assert len(_lib.SIGNATURES[name][1]) == nparams, name
+
+
+def attn(**kw):
+    """pkv_paged_attention with null buffers and valid defaults, overridden by kw."""
+    a = dict(out=None, q=None, kc=None, vc=None, bt=None, ctx=None, alibi=None, B=2, Hq=8, Hkv=2, D=128, bs=16,
+             max_blocks=4, max_seq_len=64, nb=10, scale=1.0, q_stride=1024, kbs=2 * 128 * 16, khs=128 * 16,
+             vbs=2 * 128 * 16, vhs=128 * 16, layout=_lib.PKV_LAYOUT_PAGED5D, ps=0, ws=None, ws_bytes=0,
+             qd=_lib.PKV_BF16, cd=_lib.PKV_BF16, stream=None)
+    a.update(kw)
+    lib = _lib.lib()
+    st = lib.pkv_paged_attention(*a.values())
+    return st, lib.pkv_last_error().decode()
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(Hq=6, Hkv=4), 1, "num_heads must be divisible by num_kv_heads"),
+    (dict(Hkv=0), 1, "num_heads must be divisible by num_kv_heads"),
+    (dict(max_seq_len=0), 1, "max_seq_len must be positive"),
+    (dict(max_seq_len=65), 1, "max_seq_len exceeds block table capacity"),
+    (dict(D=100), 2, "Unsupported head_size/block_size for paged_attention"),
+    (dict(bs=64, max_blocks=1), 2, "Unsupported head_size/block_size for paged_attention"),
+    (dict(qd=_lib.PKV_F16, cd=_lib.PKV_BF16), 2, "Unsupported query/cache dtype pair"),
+    (dict(qd=_lib.PKV_F32, cd=_lib.PKV_F32), 2, "Unsupported query/cache dtype pair"),
+    (dict(ps=24), 1, "partition_size must be a positive multiple of 16"),
+    (dict(ps=2048), 1, "partition_size must be a positive multiple of 16"),
+    (dict(bs=32, max_blocks=2, ps=16), 1, "partition_size must be a positive multiple of 16 and of block_size"),
+    (dict(nb=0), 1, "num_blocks must be positive"),
+    (dict(), 1, "null buffer"),
+])
+def test_paged_attention_rejections(kw, code, msg):
+    st, err = attn(**kw)
+    assert st == code and msg in err, (st, err)
+
+
+def test_paged_attention_empty_batch_is_a_noop():
+    assert attn(B=0)[0] == _lib.PKV_OK
+
+
+def test_workspace_size_closed_form():
+    lib = _lib.lib()
+    align = lambda x: (x + 255) // 256 * 256
+    # Llama-3-8B decode layer: 8 KV heads, 64 seqs -> 512-token partitions,
+    # 8 of them at max_seq_len 4096.
+    parts = 8
+    assert lib.pkv_paged_attention_workspace_size(64, 32, 8, 128, 4096, 0) == \
+        align(64 * 32 * parts * 2 * 4) + align(64 * 32 * parts * 128 * 4)
+    # One Qwen2-7B sequence at 32K: few units, so the v1 split shrinks to 256.
+    parts = 32768 // 256
+    assert lib.pkv_paged_attention_workspace_size(1, 28, 4, 128, 32768, 0) == \
+        align(28 * parts * 2 * 4) + align(28 * parts * 128 * 4)
+    # Explicit split-K partitions.
+    assert lib.pkv_paged_attention_workspace_size(4, 28, 4, 128, 131072, 512) == \
+        align(4 * 28 * 256 * 2 * 4) + align(4 * 28 * 256 * 128 * 4)
+    assert lib.pkv_paged_attention_workspace_size(4, 28, 4, 128, 100, 24) == 0
+    assert lib.pkv_paged_attention_workspace_size(4, 28, 3, 128, 100, 0) == 0
+
+
+def rac(**kw):
+    a = dict(key=None, value=None, kc=None, vc=None, slots=None, N=4, H=8, D=128, ks=1024, vs=1024,
+             layout=_lib.PKV_LAYOUT_PAGED5D, bs=16, x=8, num_slots=1024, kvd=_lib.PKV_BF16, cd=_lib.PKV_BF16,
+             stream=None)
+    a.update(kw)
+    lib = _lib.lib()
+    st = lib.pkv_reshape_and_cache(*a.values())
+    return st, lib.pkv_last_error().decode()
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(N=-1), 1, "num_tokens must be non-negative"),
+    (dict(H=0), 1, "num_kv_heads and head_size must be positive"),
+    (dict(kvd=_lib.PKV_F16, cd=_lib.PKV_BF16), 2, "Unsupported key/cache dtype pair"),
+    (dict(kvd=7), 1, "Unsupported dtype"),
+    (dict(layout=5), 1, "Unknown cache layout"),
+    (dict(num_slots=0), 1, "num_slots must be in"),
+    (dict(ks=100), 1, "row stride"),
+    (dict(x=4), 1, "16 / sizeof(cache element)"),
+    (dict(num_slots=1000), 1, "multiple of block_size"),
+    (dict(), 1, "null buffer"),
+])
+def test_reshape_and_cache_rejections(kw, code, msg):
+    st, err = rac(**kw)
+    assert st == code and msg in err, (st, err)
+
+
+def test_reshape_and_cache_empty_is_a_noop():
+    assert rac(N=0)[0] == _lib.PKV_OK
+    assert rac(N=0, layout=_lib.PKV_LAYOUT_TOKEN_MAJOR)[0] == _lib.PKV_OK
+
+
+def test_status_translation():
+    lib = _lib.lib()
+    rac(H=0)
+    with pytest.raises(ValueError, match="num_kv_heads and head_size must be positive"):
+        _lib.check(_lib.PKV_ERR_INVALID)
+    with pytest.raises(RuntimeError):
+        _lib.check(_lib.PKV_ERR_HIP)
+    _lib.check(_lib.PKV_OK)
+    assert lib.pkv_max_shared_memory_per_block(0, None) == _lib.PKV_ERR_INVALID
