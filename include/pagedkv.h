@@ -89,13 +89,13 @@ int pkv_reshape_and_cache(const void* key, const void* value,
                           int32_t cache_dtype, void* stream);
 
 /*
- * Scratch bytes that pkv_paged_attention needs for these sizes (per-partition
- * (max, sum) pairs and per-partition outputs, float32).  partition_size = 0
- * selects the single-pass (v1) semantics; the library then chooses its own
- * internal split.  The scratch needs no initialisation and is only read by
- * the launch that wrote it, so calls ordered on one stream may share one
- * buffer; calls that overlap in time must not.  Returns 0 for invalid
- * sizes.
+ * Workspace bytes that pkv_paged_attention needs for these sizes
+ * (per-partition (max, sum) pairs and per-partition outputs, float32).
+ * partition_size = 0 selects the single-pass (v1) semantics; the library
+ * then chooses its own schedule.  The workspace needs no initialisation and
+ * each launch reads only what it wrote, so calls ordered on one stream may
+ * share one buffer; calls that overlap in time must not.  Returns 0 for
+ * invalid sizes.
  */
 size_t pkv_paged_attention_workspace_size(int32_t num_seqs, int32_t num_heads,
                                           int32_t num_kv_heads,
@@ -117,8 +117,11 @@ size_t pkv_paged_attention_workspace_size(int32_t num_seqs, int32_t num_heads,
  * partition_size > 0 : split-K (paged_attention_v2): partitions of
  *                      partition_size tokens, merged by log-sum-exp.  Must be
  *                      a multiple of 16 and of block_size, at most 1024.
- * Launches: one partition kernel, plus a log-sum-exp merge kernel when the
- * call has more than one partition per sequence; both on `stream`.
+ * Launches (all on `stream`): for partition_size = 0, contexts of at most
+ * 16384 tokens and at least two (sequence, KV head) items per resident
+ * workgroup, one persistent kernel that gives each item to one workgroup,
+ * longest contexts first; otherwise a partition kernel, plus a log-sum-exp
+ * merge kernel when a sequence has more than one partition.
  * query   : [num_seqs, num_heads, head_size], row stride q_stride.
  * out     : [num_seqs, num_heads, head_size] contiguous, same dtype as query.
  * block_tables: [num_seqs, max_num_blocks_per_seq]; entries past

@@ -45,7 +45,7 @@
 
 namespace pkv {
 
-constexpr int kWaves = 4;
+constexpr int kWaves = 4;  // wavefronts per workgroup of the partition kernel
 constexpr float kLog2e = 1.4426950408889634f;
 
 __device__ __forceinline__ float wave_max(float x) {
@@ -59,14 +59,29 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
-// Two probabilities -> packed 16-bit MFMA operand word.
+// Two probabilities -> packed 16-bit MFMA operand word (hardware
+// round-to-nearest-even conversions; probabilities are never NaN).
 template <class CT> __device__ __forceinline__ uint32_t pack_p(float a, float b);
 template <> __device__ __forceinline__ uint32_t pack_p<BF16>(float a, float b) {
-  return pack2(f32_to_bf16_bits(a), f32_to_bf16_bits(b));
+  return pack2(__builtin_bit_cast(uint16_t, (__bf16)a), __builtin_bit_cast(uint16_t, (__bf16)b));
 }
 template <> __device__ __forceinline__ uint32_t pack_p<F16>(float a, float b) {
-  return pack2(f32_to_f16_bits(a), f32_to_f16_bits(b));
+  return pack2(__builtin_bit_cast(uint16_t, (_Float16)a), __builtin_bit_cast(uint16_t, (_Float16)b));
 }
+
+// 2^x with the hardware v_exp_f32 (results below 2^-126 flush to zero, which
+// no softmax weight here can notice: the largest weight of a row is >= 1).
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// The running maximum of a softmax row is only raised when a new score
+// exceeds it by more than this (log2 units): weights 2^(s - m) then stay
+// below 2^8, and the rescale of the accumulators is skipped for almost every
+// tile.  Any reference maximum gives the same normalised result.
+constexpr float kRescaleSlack = 8.f;
+
+#ifndef PKV_NBUF
+#define PKV_NBUF 4
+#endif
 
 // Query element pair -> (hi, lo) words of the cache type; q = hi + lo to
 // within 2^-16 relative, so a float32 query keeps its precision through the
@@ -87,70 +102,441 @@ template <int D> struct Tile {
   static constexpr int DT = (D + 15) / 16;      // 16-wide dimension tiles of the output
   uint4 k[KSTEPS];
   uint2 v[DT];
+  int kpb;  // block of this lane's K row (token tt0 + col), -1 if masked out
   int vpb;  // block of this lane's 4 V tokens, -1 if masked out
 };
 
-// Issues the loads of tile `tile` (tokens tt0 .. tt0+15).  Block ids that are
-// masked out (past the partition's blocks or outside the pool) read block 0
-// instead -- always in bounds -- and are discarded by the caller, so the
-// number of loads per tile is fixed and the next tile's loads can stay in
-// flight while the current one is consumed.
+// Register sets per wavefront (tiles in flight + 1), as many as leave room
+// for occupancy 2: four for a 16-bit query, head size 128 or below 120 and
+// blocks of 16 or 32 tokens (each CU then keeps 8 wavefronts x 24 KiB of
+// loads in flight); three where a float32 query (hi/lo split), per-lane
+// block ids (8-token blocks) or D = 120 need the registers; two above 128
+// and for a float32 query with 8-token blocks at D >= 120.
+template <class QT, int D, int BS> struct Prefetch {
+  static constexpr bool kF32 = std::is_same<QT, F32>::value;
+  static constexpr bool kTight = kF32 || BS < kTile || D == 120;
+  static constexpr int kBuffers = (D > 128 || (kF32 && BS < kTile && D >= 120)) ? 2 : kTight ? 3 : PKV_NBUF;
+};
+
+// Word 3 of a raw (stride 0) buffer resource on gfx9-family GPUs.
+constexpr int kBufferRsrcWord3 = 0x00020000;
+
+// Issues the loads of the tile of tokens tt0 .. tt0+15; b0 is the block of
+// tokens tt0 .. tt0+7 and b1 the block of tokens tt0+8 .. tt0+15 (-1 =
+// masked out; equal when block_size >= 16).  Both are wave-uniform.
+//
+// With block_size >= 16 the tile lies in one block: the (block, head)
+// regions of K and V become buffer resources in SGPRs, sized to the region
+// (D * block_size elements), and every lane loads at a fixed offset into
+// them.  No per-tile vector address arithmetic remains, the hardware range
+// check returns zero for anything outside the region, and a masked-out block
+// gets a zero-sized resource, so its loads return zero without touching
+// memory.
+//
+// With 8-token blocks each half of the tile has its own block; lanes then
+// address memory directly, and masked-out blocks read block 0 instead (in
+// bounds) and are discarded by the caller.  In both cases the number of
+// loads per tile is fixed, so the next tiles' loads stay in flight while the
+// current one is consumed.
 template <int D, int BS>
 __device__ __forceinline__ void load_tile(Tile<D>& t, const uint16_t* kbase, const uint16_t* vbase,
-                                          int64_t k_block_stride, int64_t v_block_stride,
-                                          const int32_t* s_blk, int nlb, int lb0, int tt0, int g, int col) {
-  constexpr int NCHUNK = D / 8;  // 16-byte K chunks per token
-  const int ktok = tt0 + col;
-  const int klb = ktok / BS - lb0;
-  const int kpb = klb < nlb ? s_blk[klb] : -1;
-  const uint16_t* kp = kbase + (int64_t)(kpb < 0 ? 0 : kpb) * k_block_stride + (ktok % BS) * 8;
+                                          int64_t k_block_stride, int64_t v_block_stride, int b0, int b1, int tt0,
+                                          int g, int col) {
+  if constexpr (BS >= kTile) {
+    const int b = b0;
+    t.kpb = t.vpb = b;
+    const int off = tt0 % BS;
+    const int64_t bb = b < 0 ? 0 : b;
+    const int bytes = b < 0 ? 0 : D * BS * 2;
+    const __amdgpu_buffer_rsrc_t kr =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(kbase + bb * k_block_stride), (short)0, bytes, kBufferRsrcWord3);
+    const __amdgpu_buffer_rsrc_t vr =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(vbase + bb * v_block_stride), (short)0, bytes, kBufferRsrcWord3);
+    // K region [D/8][BS][8]: lane (g, col), k-step j reads chunk 4j+g of
+    // token off+col.  V region [D][BS]: lane (g, col), dimension tile dt
+    // reads tokens off+4g .. +3 of dimension 16*dt + col.  The lane part of
+    // each offset is loop-invariant; the token offset within the block is
+    // wave-uniform and goes into the scalar offset.
+    const int ko = (col * 8 + g * (BS * 8)) * 2;
+    const int vo = (4 * g + col * BS) * 2;
 #pragma unroll
-  for (int j = 0; j < Tile<D>::KSTEPS; ++j) {
-    const int c = 4 * j + g;
-    if (NCHUNK % 4 == 0 || c < NCHUNK)
-      t.k[j] = *reinterpret_cast<const uint4*>(kp + c * (BS * 8));
-    else
-      t.k[j] = make_uint4(0, 0, 0, 0);
-  }
-  const int vtok = tt0 + 4 * g;
-  const int vlb = vtok / BS - lb0;
-  const int vpb = vlb < nlb ? s_blk[vlb] : -1;
-  t.vpb = vpb;
-  const uint16_t* vp = vbase + (int64_t)(vpb < 0 ? 0 : vpb) * v_block_stride + (vtok % BS);
+    for (int j = 0; j < Tile<D>::KSTEPS; ++j)
+      t.k[j] = __builtin_bit_cast(uint4,
+                                  __builtin_amdgcn_raw_buffer_load_b128(kr, ko + j * (4 * BS * 16), off * 16, 0));
 #pragma unroll
-  for (int dt = 0; dt < Tile<D>::DT; ++dt) {
-    const int d = 16 * dt + col;
-    if (D % 16 == 0 || d < D)
-      t.v[dt] = *reinterpret_cast<const uint2*>(vp + d * BS);
-    else
-      t.v[dt] = make_uint2(0, 0);
+    for (int dt = 0; dt < Tile<D>::DT; ++dt)
+      t.v[dt] = __builtin_bit_cast(uint2,
+                                   __builtin_amdgcn_raw_buffer_load_b64(vr, vo + dt * (16 * BS * 2), off * 2, 0));
+  } else {
+    constexpr int NCHUNK = D / 8;  // 16-byte K chunks per token
+    const int kpb = col < 8 ? b0 : b1;  // K row = token tt0 + col
+    t.kpb = kpb;
+    const uint16_t* kp = kbase + (int64_t)(kpb < 0 ? 0 : kpb) * k_block_stride + (col % BS) * 8;
+    const int vpb = g < 2 ? b0 : b1;     // V tokens tt0 + 4g .. +3
+    t.vpb = vpb;
+    const uint16_t* vp = vbase + (int64_t)(vpb < 0 ? 0 : vpb) * v_block_stride + ((4 * g) % BS);
+#pragma unroll
+    for (int j = 0; j < Tile<D>::KSTEPS; ++j) {
+      const int c = 4 * j + g;
+      if (NCHUNK % 4 == 0 || c < NCHUNK)
+        t.k[j] = *reinterpret_cast<const uint4*>(kp + c * (BS * 8));
+      else
+        t.k[j] = make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int dt = 0; dt < Tile<D>::DT; ++dt) {
+      const int d = 16 * dt + col;
+      if (D % 16 == 0 || d < D)
+        t.v[dt] = *reinterpret_cast<const uint2*>(vp + d * BS);
+      else
+        t.v[dt] = make_uint2(0, 0);
+    }
   }
 }
 
+// Block ids of the tiles one wavefront streams, held lane-indexed in a few
+// VGPRs so that each tile's ids reach SGPRs with a v_readlane: entry e =
+// 64 * c + lane of array c is block half e % PER_TILE of the wavefront's
+// tile number e / PER_TILE (0-based in the order the wavefront takes them).
+// MAXT bounds the tiles per wavefront.
+template <int BS, int MAXT> struct WaveBlocks {
+  static constexpr int PER_TILE = BS >= kTile ? 1 : 2;
+  static constexpr int N = (MAXT * PER_TILE + 63) / 64;
+  int v[N];
+
+  // Tiles first, first + nw, ... of tokens [t0, t1) of the block-table row
+  // `row`, whose blocks lb0 .. lb0+nlb-1 cover the range.  Ids outside
+  // [0, num_blocks) become -1.
+  __device__ __forceinline__ void load(const int32_t* row, int64_t num_blocks, int nlb, int lb0, int t0, int first,
+                                       int nw, int lane) {
+#pragma unroll
+    for (int c = 0; c < N; ++c) {
+      const int e = 64 * c + lane;
+      const int tile = first + (e / PER_TILE) * nw;
+      const int lb = (t0 + tile * kTile + (e % PER_TILE) * 8) / BS - lb0;
+      int b = -1;
+      if (lb < nlb) {
+        b = row[lb0 + lb];
+        b = (int64_t)(uint32_t)b < num_blocks ? b : -1;
+      }
+      v[c] = b;
+    }
+  }
+  // Block of entry e (wave-uniform e).
+  __device__ __forceinline__ int get(int e) const {
+    const int c = e >> 6, l = e & 63;
+    int r = __builtin_amdgcn_readlane(v[0], l);
+#pragma unroll
+    for (int i = 1; i < N; ++i)
+      if (c == i) r = __builtin_amdgcn_readlane(v[i], l);
+    return r;
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Shared pieces of the two decode kernels.
+// ---------------------------------------------------------------------------
+
+// One wavefront's softmax state: unnormalised output (MFMA accumulator
+// layout: lane l, register r of tile dt = head l%16, dim 16*dt + 4*(l/16) + r),
+// the reference maximum the weights are taken against, the weight sum of
+// this lane's 4 tokens per tile, and the true running maximum.
+template <int D> struct WaveAcc {
+  f32x4 o[Tile<D>::DT];
+  float m_run, l_run, m_max;
+  __device__ __forceinline__ void init() {
+#pragma unroll
+    for (int dt = 0; dt < Tile<D>::DT; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    m_run = -INFINITY;
+    l_run = 0.f;
+    m_max = -INFINITY;
+  }
+};
+
+// Query rows h0 .. h0+nh-1 of sequence seq -> B-operand registers (head =
+// col, dims 32j + 8g .. +8); a float32 query is split into hi + lo words.
+template <class QT, class CT, int D>
+__device__ __forceinline__ void load_query(const DecodeParams& p, int seq, int h0, int nh, int g, int col,
+                                           uint4 (&qa)[Tile<D>::KSTEPS],
+                                           uint4 (&qb)[std::is_same<QT, F32>::value ? Tile<D>::KSTEPS : 1]) {
+  using QS = typename Elem<QT>::storage;
+  constexpr bool SPLIT_Q = std::is_same<QT, F32>::value;
+  const QS* qrow = static_cast<const QS*>(p.q) + (int64_t)seq * p.q_stride + (int64_t)(h0 + col) * D;
+#pragma unroll
+  for (int j = 0; j < Tile<D>::KSTEPS; ++j) {
+    const int d0 = 32 * j + 8 * g;
+    uint4 a = make_uint4(0, 0, 0, 0), b = make_uint4(0, 0, 0, 0);
+    if (col < nh && d0 < D) {
+      if constexpr (SPLIT_Q) {
+        const float4 x0 = *reinterpret_cast<const float4*>(qrow + d0);
+        const float4 x1 = *reinterpret_cast<const float4*>(qrow + d0 + 4);
+        uint32_t h[8], l[8];
+        split_q<CT>(x0.x, h[0], l[0]);
+        split_q<CT>(x0.y, h[1], l[1]);
+        split_q<CT>(x0.z, h[2], l[2]);
+        split_q<CT>(x0.w, h[3], l[3]);
+        split_q<CT>(x1.x, h[4], l[4]);
+        split_q<CT>(x1.y, h[5], l[5]);
+        split_q<CT>(x1.z, h[6], l[6]);
+        split_q<CT>(x1.w, h[7], l[7]);
+        a = make_uint4(pack2(h[0], h[1]), pack2(h[2], h[3]), pack2(h[4], h[5]), pack2(h[6], h[7]));
+        b = make_uint4(pack2(l[0], l[1]), pack2(l[2], l[3]), pack2(l[4], l[5]), pack2(l[6], l[7]));
+      } else {
+        a = *reinterpret_cast<const uint4*>(qrow + d0);
+      }
+    }
+    qa[j] = a;
+    if constexpr (SPLIT_Q) qb[j] = b;
+  }
+}
+
+// Streams the 16-token tiles first, first+NW, ... of tokens [t0, t1) of one
+// (sequence, KV head) through the online softmax into acc.  blk holds the
+// wavefront's block ids (WaveBlocks::load with the same first, NW, t0);
+// first must be wave-uniform.  Tiles that lie entirely inside the range go
+// through a prefetching loop; the one tile that crosses t1 (if any) is
+// consumed last, with masking, by the wavefront it belongs to.
+template <class QT, class CT, int D, int BS, int NW, int MAXT>
+__device__ __forceinline__ void stream_tiles(const DecodeParams& p, const uint16_t* kbase, const uint16_t* vbase,
+                                             const WaveBlocks<BS, MAXT>& blk, int t0, int t1, uint32_t ctx,
+                                             int first, int g, int col, const uint4 (&qa)[Tile<D>::KSTEPS],
+                                             const uint4 (&qb)[std::is_same<QT, F32>::value ? Tile<D>::KSTEPS : 1],
+                                             float slope, WaveAcc<D>& acc) {
+  constexpr int KSTEPS = Tile<D>::KSTEPS;
+  constexpr int DT = Tile<D>::DT;
+  constexpr bool SPLIT_Q = std::is_same<QT, F32>::value;
+  constexpr int PT = WaveBlocks<BS, MAXT>::PER_TILE;
+  const int ntiles = (t1 - t0 + kTile - 1) / kTile;
+  const int nfull = (t1 - t0) / kTile;  // tiles entirely inside [t0, t1)
+  if (first >= ntiles) return;
+
+  // Loads per tile, and the wait that leaves only the newer tiles' loads in
+  // flight.  Waiting for the current tile's loads explicitly (instead of
+  // letting each use wait) also tells the compiler that every older load has
+  // landed, so reusing registers across the loop back-edge costs no drain.
+  constexpr int NBUF = Prefetch<QT, D, BS>::kBuffers;
+  constexpr int LOADS = KSTEPS + DT;
+  constexpr int AHEAD = (NBUF - 1) * LOADS;
+  static_assert(AHEAD < 64, "vmcnt counts at most 63 outstanding loads");
+  // s_waitcnt immediate (gfx9 encoding): vmcnt in bits 3:0 and 15:14,
+  // expcnt 6:4 and lgkmcnt 11:8 left at their maxima (no wait).
+  constexpr int kWaitAhead = (AHEAD & 15) | ((AHEAD >> 4) << 14) | (7 << 4) | (15 << 8);
+
+  // Consumes one loaded tile starting at token tt0.  TAIL: the tile crosses
+  // t1, so tokens at or past t1 are masked.  Tokens of masked-out blocks
+  // contribute nothing either.  Masked tokens get score -inf and V zero (a
+  // slot may hold anything, including NaN); with block_size >= 16 a masked
+  // block's loads already returned zero, so only its scores need masking.
+  auto consume = [&](auto tail_tag, Tile<D>& t, int tt0) {
+    constexpr bool TAIL = decltype(tail_tag)::value;
+    const int vtok = tt0 + 4 * g;
+    bool zero_v = false;
+    if constexpr (TAIL) {
+      zero_v = true;
+    } else if constexpr (BS < kTile) {
+      zero_v = !__all(t.vpb >= 0 && t.kpb >= 0);
+    }
+    if (zero_v) {
+      const uint32_t ok = t.vpb >= 0 ? 0xffffffffu : 0u;
+      const uint32_t m01 = ok & ((vtok + 0 < t1 ? 0x0000ffffu : 0u) | (vtok + 1 < t1 ? 0xffff0000u : 0u));
+      const uint32_t m23 = ok & ((vtok + 2 < t1 ? 0x0000ffffu : 0u) | (vtok + 3 < t1 ? 0xffff0000u : 0u));
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        t.v[dt].x &= m01;
+        t.v[dt].y &= m23;
+      }
+    }
+    // ---- S^T = K * Q^T ----
+    f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < KSTEPS; ++j) {
+      sacc = Mma<CT>::k32(t.k[j], qa[j], sacc);
+      if constexpr (SPLIT_Q) sacc = Mma<CT>::k32(t.k[j], qb[j], sacc);
+    }
+    // ---- online softmax (log2 domain) ----
+    float sc[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sc[r] = sacc[r] * p.scale_log2;
+    if (p.alibi != nullptr) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sc[r] += slope * (float)(vtok + r - (int)ctx + 1);
+    }
+    if (TAIL || zero_v) {
+      // Lane (g, col) holds scores of tokens vtok..vtok+3 for head col; the K
+      // row of token tt0 + i was loaded by lane col = i.
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int krow_ok = __shfl(t.kpb, 4 * g + r, 16) >= 0;
+        sc[r] = (vtok + r < t1 && t.vpb >= 0 && krow_ok) ? sc[r] : -INFINITY;
+      }
+    } else if constexpr (BS >= kTile) {
+      if (t.vpb < 0) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sc[r] = -INFINITY;
+      }
+    }
+    const float mt = column_max(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
+    acc.m_max = fmaxf(acc.m_max, mt);
+    if (__any(mt > acc.m_run + kRescaleSlack)) {
+      const float m_new = fmaxf(acc.m_run, mt);
+      const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(acc.m_run - m_new);
+      acc.l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) acc.o[dt] *= alpha;
+      acc.m_run = m_new;
+    }
+    const float m_use = acc.m_run == -INFINITY ? 0.f : acc.m_run;
+    float pr[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) pr[r] = fast_exp2(sc[r] - m_use);
+    acc.l_run += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+    // ---- O^T += V^T * P^T ----
+    const uint2 pp = make_uint2(pack_p<CT>(pr[0], pr[1]), pack_p<CT>(pr[2], pr[3]));
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) acc.o[dt] = Mma<CT>::k16(t.v[dt], pp, acc.o[dt]);
+  };
+  using Full = std::integral_constant<bool, false>;
+  using Tail = std::integral_constant<bool, true>;
+  auto load = [&](Tile<D>& t, int tile) {
+    const int k = (tile - first) / NW;
+    const int b0 = blk.get(k * PT);
+    const int b1 = PT == 2 ? blk.get(k * PT + 1) : b0;
+    load_tile<D, BS>(t, kbase, vbase, p.k_block_stride, p.v_block_stride, b0, b1, t0 + tile * kTile, g, col);
+  };
+
+  // Full tiles: NBUF register sets, the loads of the wavefront's tile
+  // i + NW*(NBUF-1) issued before tile i is consumed, so each wavefront keeps
+  // NBUF - 1 tiles in flight.  Past its last full tile a wavefront re-reads
+  // that tile (in bounds, served by L2) so that every iteration issues the
+  // same loads.  (Driving the loop by the tile index rather than a 0-based
+  // per-wavefront counter keeps the compiler's register allocation of the
+  // rotating tile sets tight.)
+  if (first < nfull) {
+    const int last = first + ((nfull - 1 - first) / NW) * NW;
+    Tile<D> t[NBUF];
+#pragma unroll
+    for (int b = 0; b < NBUF - 1; ++b) load(t[b], min(first + b * NW, last));
+    int tile = first;
+    while (true) {
+#pragma unroll
+      for (int b = 0; b < NBUF; ++b) {
+        load(t[(b + NBUF - 1) % NBUF], min(tile + (NBUF - 1) * NW, last));
+        __builtin_amdgcn_s_waitcnt(kWaitAhead);
+        consume(Full{}, t[b], t0 + tile * kTile);
+        tile += NW;
+        if (tile >= nfull) break;
+      }
+      if (tile >= nfull) break;
+    }
+  }
+  // The tile that crosses t1, if this wavefront owns it.
+  if (nfull < ntiles && nfull >= first && (nfull - first) % NW == 0) {
+    Tile<D> tt;
+    load(tt, nfull);
+    consume(Tail{}, tt, t0 + nfull * kTile);
+  }
+}
+
+// Merges the NW wavefronts' states of one workgroup.  Every wavefront first
+// moves its accumulators onto its true maximum, so that the final
+// denominator is sum(exp(s - max)) + 1e-6 exactly as the reference's.  On
+// return wavefront 0 holds the merged output in acc.o, the maximum in M and
+// the weight sum in L (per column); other wavefronts' results are
+// undefined.  Contains one workgroup barrier.
+template <int D, int NW>
+__device__ __forceinline__ void merge_waves(WaveAcc<D>& acc, float (*s_red)[Tile<D>::DT * 4][64],
+                                            float (*s_m)[16], float (*s_l)[16], int wave, int lane, int g, int col,
+                                            float& M, float& L) {
+  constexpr int DT = Tile<D>::DT;
+  if (acc.m_max != -INFINITY && acc.m_max != acc.m_run) {
+    const float f = exp2f(acc.m_run - acc.m_max);
+    acc.l_run *= f;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) acc.o[dt] *= f;
+    acc.m_run = acc.m_max;
+  }
+  const float l_col = column_sum(acc.l_run);
+  if (wave > 0) {
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s_red[wave - 1][dt * 4 + r][lane] = acc.o[dt][r];
+  }
+  if (g == 0) {
+    s_m[wave][col] = acc.m_run;
+    s_l[wave][col] = l_col;
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  M = acc.m_run;
+#pragma unroll
+  for (int w = 1; w < NW; ++w) M = fmaxf(M, s_m[w][col]);
+  const float mu = M == -INFINITY ? 0.f : M;
+  const float a0 = exp2f(acc.m_run - mu);
+  L = l_col * a0;
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) acc.o[dt] *= a0;
+#pragma unroll
+  for (int w = 1; w < NW; ++w) {
+    const float aw = exp2f(s_m[w][col] - mu);
+    L += s_l[w][col] * aw;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc.o[dt][r] += aw * s_red[w - 1][dt * 4 + r][lane];
+  }
+}
+
+// Writes out[row] = o / (L + 1e-6) from wavefront 0's merged state.
+template <class QT, int D>
+__device__ __forceinline__ void write_output(const DecodeParams& p, int64_t hrow, const WaveAcc<D>& acc, float L,
+                                             int g) {
+  using QS = typename Elem<QT>::storage;
+  const float inv = 1.f / (L + 1e-6f);
+  QS* out = static_cast<QS*>(p.out) + hrow * D;
+#pragma unroll
+  for (int dt = 0; dt < Tile<D>::DT; ++dt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int d = 16 * dt + 4 * g + r;
+      if (D % 16 == 0 || d < D) out[d] = from_f32<QT>(acc.o[dt][r] * inv);
+    }
+}
+
+__device__ __forceinline__ void unit_heads(const DecodeParams& p, int unit, int& kvh, int& h0, int& nh) {
+  kvh = unit / p.slices;
+  const int slice = unit - kvh * p.slices;
+  h0 = kvh * p.group + slice * 16;
+  nh = min(16, p.group - slice * 16);
+}
+
+// ---------------------------------------------------------------------------
+// Partition kernel: one workgroup of 4 wavefronts per (partition, sequence,
+// unit).
+// ---------------------------------------------------------------------------
 template <class QT, class CT, int D, int BS>
 __global__ __launch_bounds__(256) void paged_decode_part_kernel(DecodeParams p) {
   using QS = typename Elem<QT>::storage;
   constexpr int KSTEPS = Tile<D>::KSTEPS;
   constexpr int DT = Tile<D>::DT;
   constexpr bool SPLIT_Q = std::is_same<QT, F32>::value;
+  constexpr int MAXT = kMaxPartition / kTile / kWaves;  // tiles per wavefront
 
-  __shared__ int32_t s_blk[kMaxPartition / BS];
   __shared__ float s_red[kWaves - 1][DT * 4][64];
   __shared__ float s_m[kWaves][16];
   __shared__ float s_l[kWaves][16];
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, col = lane & 15;
 
   const int unit = blockIdx.x % p.units;
   const int rest = blockIdx.x / p.units;
   const int seq = rest % p.num_seqs;
   const int part = rest / p.num_seqs;
-  const int kvh = unit / p.slices;
-  const int slice = unit - kvh * p.slices;
-  const int h0 = kvh * p.group + slice * 16;
-  const int nh = min(16, p.group - slice * 16);
+  int kvh, h0, nh;
+  unit_heads(p, unit, kvh, h0, nh);
 
   // Context lengths are read as unsigned, as the reference does.
   const uint32_t ctx = (uint32_t)p.context_lens[seq];
@@ -168,177 +554,25 @@ __global__ __launch_bounds__(256) void paged_decode_part_kernel(DecodeParams p) 
   const int lb0 = t0 / BS;
   const int nlb = (t1 + BS - 1) / BS - lb0;
 
-  // Block-table slice of this partition -> LDS (one coalesced read).
-  {
-    const int32_t* bt = p.block_tables + (int64_t)seq * p.max_blocks_per_seq + lb0;
-    for (int i = tid; i < nlb; i += 256) {
-      const int32_t b = bt[i];
-      s_blk[i] = ((int64_t)(uint32_t)b < p.num_blocks) ? b : -1;
-    }
-  }
-
-  // Query group -> B operand registers (head = col, dims 32j + 8g .. +8).
+  WaveBlocks<BS, MAXT> blk;
+  blk.load(p.block_tables + (int64_t)seq * p.max_blocks_per_seq, p.num_blocks, nlb, lb0, t0, wave, kWaves, lane);
   uint4 qa[KSTEPS];
   uint4 qb[SPLIT_Q ? KSTEPS : 1];
-  {
-    const QS* qrow = static_cast<const QS*>(p.q) + (int64_t)seq * p.q_stride + (int64_t)(h0 + col) * D;
-#pragma unroll
-    for (int j = 0; j < KSTEPS; ++j) {
-      const int d0 = 32 * j + 8 * g;
-      uint4 a = make_uint4(0, 0, 0, 0), b = make_uint4(0, 0, 0, 0);
-      if (col < nh && d0 < D) {
-        if constexpr (SPLIT_Q) {
-          const float4 x0 = *reinterpret_cast<const float4*>(qrow + d0);
-          const float4 x1 = *reinterpret_cast<const float4*>(qrow + d0 + 4);
-          uint32_t h[8], l[8];
-          split_q<CT>(x0.x, h[0], l[0]);
-          split_q<CT>(x0.y, h[1], l[1]);
-          split_q<CT>(x0.z, h[2], l[2]);
-          split_q<CT>(x0.w, h[3], l[3]);
-          split_q<CT>(x1.x, h[4], l[4]);
-          split_q<CT>(x1.y, h[5], l[5]);
-          split_q<CT>(x1.z, h[6], l[6]);
-          split_q<CT>(x1.w, h[7], l[7]);
-          a = make_uint4(pack2(h[0], h[1]), pack2(h[2], h[3]), pack2(h[4], h[5]), pack2(h[6], h[7]));
-          b = make_uint4(pack2(l[0], l[1]), pack2(l[2], l[3]), pack2(l[4], l[5]), pack2(l[6], l[7]));
-        } else {
-          a = *reinterpret_cast<const uint4*>(qrow + d0);
-        }
-      }
-      qa[j] = a;
-      if constexpr (SPLIT_Q) qb[j] = b;
-    }
-  }
+  load_query<QT, CT, D>(p, seq, h0, nh, g, col, qa, qb);
   const float slope = (p.alibi != nullptr && col < nh) ? p.alibi[h0 + col] * kLog2e : 0.f;
-  __syncthreads();
 
-  f32x4 o[DT];
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY, l_run = 0.f;
-
+  WaveAcc<D> acc;
+  acc.init();
   const uint16_t* kbase = static_cast<const uint16_t*>(p.k_cache) + (int64_t)kvh * p.k_head_stride;
   const uint16_t* vbase = static_cast<const uint16_t*>(p.v_cache) + (int64_t)kvh * p.v_head_stride;
-  const int ntiles = (t1 - t0 + kTile - 1) / kTile;
+  stream_tiles<QT, CT, D, BS, kWaves, MAXT>(p, kbase, vbase, blk, t0, t1, ctx, wave, g, col, qa, qb, slope, acc);
 
-  // Consumes one loaded tile starting at token tt0.
-  auto consume = [&](Tile<D>& t, int tt0) {
-    const int vtok = tt0 + 4 * g;
-    // Tokens at or past the end of the partition, and tokens of masked-out
-    // blocks, contribute nothing: zero their V (the slots may hold anything,
-    // including NaN) and their scores.
-    if (t.vpb < 0) {
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) t.v[dt] = make_uint2(0, 0);
-    } else if (tt0 + kTile > t1) {
-      const uint32_t m01 = (vtok + 0 < t1 ? 0x0000ffffu : 0u) | (vtok + 1 < t1 ? 0xffff0000u : 0u);
-      const uint32_t m23 = (vtok + 2 < t1 ? 0x0000ffffu : 0u) | (vtok + 3 < t1 ? 0xffff0000u : 0u);
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        t.v[dt].x &= m01;
-        t.v[dt].y &= m23;
-      }
-    }
-    // ---- S^T = K * Q^T ----
-    f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int j = 0; j < KSTEPS; ++j) {
-      sacc = Mma<CT>::k32(t.k[j], qa[j], sacc);
-      if constexpr (SPLIT_Q) sacc = Mma<CT>::k32(t.k[j], qb[j], sacc);
-    }
-    // ---- online softmax (log2 domain) ----
-    float sc[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int tok = vtok + r;
-      float x = sacc[r] * p.scale_log2;
-      if (p.alibi != nullptr) x += slope * (float)(tok - (int)ctx + 1);
-      sc[r] = (tok < t1 && t.vpb >= 0) ? x : -INFINITY;
-    }
-    const float mt = column_max(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
-    const float m_new = fmaxf(m_run, mt);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = exp2f(m_run - m_use);
-    float pr[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) pr[r] = exp2f(sc[r] - m_use);
-    l_run = l_run * alpha + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
-    m_run = m_new;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) o[dt] *= alpha;
-    // ---- O^T += V^T * P^T ----
-    const uint2 pp = make_uint2(pack_p<CT>(pr[0], pr[1]), pack_p<CT>(pr[2], pr[3]));
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) o[dt] = Mma<CT>::k16(t.v[dt], pp, o[dt]);
-  };
-
-  // Two register sets: the loads of tile i+4 are issued before tile i is
-  // consumed.  Past the last tile the prefetch re-reads the current tile
-  // (in bounds, served by L2) so that every iteration issues the same loads.
-  if (wave < ntiles) {
-    Tile<D> ta, tb;
-    int tile = wave;
-    load_tile<D, BS>(ta, kbase, vbase, p.k_block_stride, p.v_block_stride, s_blk, nlb, lb0, t0 + tile * kTile,
-                     g, col);
-    while (true) {
-      int nt = tile + kWaves < ntiles ? tile + kWaves : tile;
-      load_tile<D, BS>(tb, kbase, vbase, p.k_block_stride, p.v_block_stride, s_blk, nlb, lb0, t0 + nt * kTile,
-                       g, col);
-      consume(ta, t0 + tile * kTile);
-      tile += kWaves;
-      if (tile >= ntiles) break;
-      nt = tile + kWaves < ntiles ? tile + kWaves : tile;
-      load_tile<D, BS>(ta, kbase, vbase, p.k_block_stride, p.v_block_stride, s_blk, nlb, lb0, t0 + nt * kTile,
-                       g, col);
-      consume(tb, t0 + tile * kTile);
-      tile += kWaves;
-      if (tile >= ntiles) break;
-    }
-  }
-
-  // ---- merge the four wavefronts of the workgroup ----
-  const float l_col = column_sum(l_run);
-  if (wave > 0) {
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) s_red[wave - 1][dt * 4 + r][lane] = o[dt][r];
-  }
-  if (g == 0) {
-    s_m[wave][col] = m_run;
-    s_l[wave][col] = l_col;
-  }
-  __syncthreads();
-  if (wave != 0) return;
-  float M = m_run;
-#pragma unroll
-  for (int w = 1; w < kWaves; ++w) M = fmaxf(M, s_m[w][col]);
-  const float mu = M == -INFINITY ? 0.f : M;
-  const float a0 = exp2f(m_run - mu);
-  float L = l_col * a0;
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt) o[dt] *= a0;
-#pragma unroll
-  for (int w = 1; w < kWaves; ++w) {
-    const float aw = exp2f(s_m[w][col] - mu);
-    L += s_l[w][col] * aw;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) o[dt][r] += aw * s_red[w - 1][dt * 4 + r][lane];
-  }
-  if (col >= nh) return;
+  float M, L;
+  merge_waves<D, kWaves>(acc, s_red, s_m, s_l, wave, lane, g, col, M, L);
+  if (wave != 0 || col >= nh) return;
   const int64_t hrow = (int64_t)seq * p.num_heads + h0 + col;
   if (nparts == 1) {
-    const float inv = 1.f / (L + 1e-6f);
-    QS* out = static_cast<QS*>(p.out) + hrow * D;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int d = 16 * dt + 4 * g + r;
-        if (D % 16 == 0 || d < D) out[d] = from_f32<QT>(o[dt][r] * inv);
-      }
+    write_output<QT, D>(p, hrow, acc, L, g);
     return;
   }
   const int64_t slot = hrow * p.max_parts + part;
@@ -349,9 +583,149 @@ __global__ __launch_bounds__(256) void paged_decode_part_kernel(DecodeParams p) 
     const int d = 16 * dt + 4 * g;
     if (D % 16 == 0 || d < D)
       *reinterpret_cast<float4*>(wo + d) =
-          make_float4(o[dt][0] * invl, o[dt][1] * invl, o[dt][2] * invl, o[dt][3] * invl);
+          make_float4(acc.o[dt][0] * invl, acc.o[dt][1] * invl, acc.o[dt][2] * invl, acc.o[dt][3] * invl);
   }
   if (g == 0) *reinterpret_cast<float2*>(p.ws_ml + slot * 2) = make_float2(M, L);
+}
+
+// ---------------------------------------------------------------------------
+// Persistent kernel: one workgroup of NW wavefronts per CU works through
+// whole (sequence, unit) items and produces their output rows without any
+// partial results.  Items are ranked longest context first and dealt in a
+// snake order (round k gives rank k*G + w to workgroup w, reversed on odd
+// rounds), which balances the workgroups' total work.  While a workgroup
+// streams one item it already loads the next item's context length, block
+// ids and query, so consecutive items follow each other without a gap.
+// ---------------------------------------------------------------------------
+template <int D> struct Persist {
+  // Wavefronts per workgroup: two per SIMD while the register budget allows
+  // (head sizes up to 128), one above.
+  static constexpr int kWaves = D <= 128 ? 8 : 4;
+};
+
+struct PersistItem {
+  int seq, kvh, h0, nh;
+  uint32_t ctx;
+  bool live;  // context in (0, max_seq_len]; otherwise the rows are zero
+};
+
+template <class QT, class CT, int D, int BS>
+__global__ __launch_bounds__(64 * Persist<D>::kWaves) void paged_decode_persist_kernel(DecodeParams p) {
+  constexpr int NW = Persist<D>::kWaves;
+  constexpr int NT = 64 * NW;
+  constexpr int KSTEPS = Tile<D>::KSTEPS;
+  constexpr int DT = Tile<D>::DT;
+  constexpr bool SPLIT_Q = std::is_same<QT, F32>::value;
+  constexpr int MAXT = kPersistMaxSeq / kTile / NW;  // tiles per wavefront
+
+  __shared__ float s_red[2][NW - 1][DT * 4][64];
+  __shared__ float s_m[2][NW][16];
+  __shared__ float s_l[2][NW][16];
+  __shared__ uint32_t s_ctx[kPersistMaxOrder];
+  __shared__ int32_t s_order[kPersistMaxOrder];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, col = lane & 15;
+  const int B = p.num_seqs;
+  const int total = B * p.units;
+  const int G = gridDim.x;
+
+  // Longest-first rank of the sequences (ties by index).  Empty and
+  // over-long contexts (zero rows) count as length 0.
+  const bool ordered = B <= kPersistMaxOrder;
+  if (ordered) {
+    for (int s = tid; s < B; s += NT) {
+      const uint32_t c = (uint32_t)p.context_lens[s];
+      s_ctx[s] = c > (uint32_t)p.max_seq_len ? 0u : c;
+    }
+    __syncthreads();
+    for (int s = tid; s < B; s += NT) {
+      const uint32_t c = s_ctx[s];
+      int r = 0;
+      for (int s2 = 0; s2 < B; ++s2) {
+        const uint32_t c2 = s_ctx[s2];
+        r += (c2 > c) || (c2 == c && s2 < s);
+      }
+      s_order[r] = s;
+    }
+    __syncthreads();
+  }
+  // Rank of this workgroup's k-th item (>= total: none).
+  auto rank_of = [&](int k) { return k * G + ((k & 1) ? G - 1 - (int)blockIdx.x : (int)blockIdx.x); };
+  auto item_at = [&](int rank) {
+    PersistItem it;
+    const int sr = rank / p.units;
+    const int unit = rank - sr * p.units;
+    it.seq = ordered ? s_order[sr] : sr;
+    unit_heads(p, unit, it.kvh, it.h0, it.nh);
+    it.ctx = (uint32_t)p.context_lens[it.seq];
+    it.live = it.ctx != 0 && it.ctx <= (uint32_t)p.max_seq_len;
+    return it;
+  };
+  // Block ids of the wavefront's tiles of an item.  The bound comes from
+  // max_seq_len rather than the item's context, so these loads do not wait
+  // for it; entries past the context are never used.
+  const int nlb_max = (p.max_seq_len + BS - 1) / BS;
+  auto load_blocks = [&](int seq, WaveBlocks<BS, MAXT>& blk) {
+    blk.load(p.block_tables + (int64_t)seq * p.max_blocks_per_seq, p.num_blocks, nlb_max, 0, 0, wave, NW, lane);
+  };
+
+  int k = 0;
+  const int rank = rank_of(0);
+  if (rank >= total) return;
+  PersistItem it = item_at(rank);
+  WaveBlocks<BS, MAXT> blk;
+  load_blocks(it.seq, blk);
+  uint4 qa[KSTEPS];
+  uint4 qb[SPLIT_Q ? KSTEPS : 1];
+  load_query<QT, CT, D>(p, it.seq, it.h0, it.nh, g, col, qa, qb);
+  float slope = (p.alibi != nullptr && col < it.nh) ? p.alibi[it.h0 + col] * kLog2e : 0.f;
+
+  int buf = 0;
+  while (true) {
+    // Next item's metadata, loaded now and used after this item.
+    const int nrank = rank_of(k + 1);
+    const bool has_next = nrank < total;
+    PersistItem nit = it;
+    WaveBlocks<BS, MAXT> nblk;
+    uint4 nqa[KSTEPS];
+    uint4 nqb[SPLIT_Q ? KSTEPS : 1];
+    float nslope = 0.f;
+    if (has_next) {
+      nit = item_at(nrank);
+      load_blocks(nit.seq, nblk);
+      load_query<QT, CT, D>(p, nit.seq, nit.h0, nit.nh, g, col, nqa, nqb);
+      nslope = (p.alibi != nullptr && col < nit.nh) ? p.alibi[nit.h0 + col] * kLog2e : 0.f;
+    }
+
+    WaveAcc<D> acc;
+    acc.init();
+    if (it.live) {
+      const uint16_t* kbase = static_cast<const uint16_t*>(p.k_cache) + (int64_t)it.kvh * p.k_head_stride;
+      const uint16_t* vbase = static_cast<const uint16_t*>(p.v_cache) + (int64_t)it.kvh * p.v_head_stride;
+      stream_tiles<QT, CT, D, BS, NW, MAXT>(p, kbase, vbase, blk, 0, (int)it.ctx, it.ctx, wave, g, col, qa, qb,
+                                            slope, acc);
+    }
+    float M, L;
+    // s_red[buf] is written again two items later, after the next item's
+    // barrier, which wavefront 0 reaches only once it has read it.
+    merge_waves<D, NW>(acc, s_red[buf], s_m[buf], s_l[buf], wave, lane, g, col, M, L);
+    if (wave == 0 && col < it.nh) write_output<QT, D>(p, (int64_t)it.seq * p.num_heads + it.h0 + col, acc, L, g);
+    if (!has_next) break;
+    it = nit;
+    blk = nblk;
+#pragma unroll
+    for (int j = 0; j < KSTEPS; ++j) qa[j] = nqa[j];
+    if constexpr (SPLIT_Q) {
+#pragma unroll
+      for (int j = 0; j < KSTEPS; ++j) qb[j] = nqb[j];
+    }
+    slope = nslope;
+    buf ^= 1;
+    ++k;
+  }
 }
 
 // Log-sum-exp merge of the partitions of one (sequence, query head) per
@@ -379,14 +753,26 @@ __global__ __launch_bounds__(256) void paged_decode_reduce_kernel(DecodeParams p
 #pragma unroll
   for (int i = 0; i < NDL; ++i) acc[i] = 0.f;
   float sum = 0.f;
-  for (int i = 0; i < nparts; ++i) {
-    const float2 e = *reinterpret_cast<const float2*>(ml + 2 * i);
-    const float w = e.y * exp2f(e.x - mu);
-    sum += w;
+  // Eight partitions per step, their loads issued together.
+  for (int i0 = 0; i0 < nparts; i0 += 8) {
+    float2 e[8];
+    float ov[8][NDL];
 #pragma unroll
-    for (int k = 0; k < NDL; ++k) {
-      const int d = lane + 64 * k;
-      if (D % 64 == 0 || d < D) acc[k] += w * po[(int64_t)i * D + d];
+    for (int u = 0; u < 8; ++u) {
+      const int i = min(i0 + u, nparts - 1);
+      e[u] = *reinterpret_cast<const float2*>(ml + 2 * i);
+#pragma unroll
+      for (int k = 0; k < NDL; ++k) {
+        const int d = lane + 64 * k;
+        ov[u][k] = (D % 64 == 0 || d < D) ? po[(int64_t)i * D + d] : 0.f;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const float w = i0 + u < nparts ? e[u].y * exp2f(e[u].x - mu) : 0.f;
+      sum += w;
+#pragma unroll
+      for (int k = 0; k < NDL; ++k) acc[k] += w * ov[u][k];
     }
   }
   const float inv = 1.f / (sum + 1e-6f);
@@ -398,8 +784,48 @@ __global__ __launch_bounds__(256) void paged_decode_reduce_kernel(DecodeParams p
   }
 }
 
+// ---------------------------------------------------------------------------
+// Launchers
+// ---------------------------------------------------------------------------
+
+// Multiprocessor count of the current device, cached per device.
+inline int device_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
 template <class QT, class CT, int D, int BS>
 static hipError_t launch_one(const DecodeParams& p, hipStream_t stream) {
+  if (p.persistent) {
+    constexpr int NT = 64 * Persist<D>::kWaves;
+    static int per_cu = -1;  // resident workgroups per CU for this instantiation
+    if (per_cu < 0) {
+      int n = 0;
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, paged_decode_persist_kernel<QT, CT, D, BS>, NT, 0) !=
+              hipSuccess ||
+          n <= 0)
+        n = 1;
+      per_cu = n;
+    }
+    // Whole (sequence, unit) items balance well once there are at least two
+    // per resident workgroup; fewer, longer items go to the partition path.
+    // The grid never exceeds what is resident at once, which the snake
+    // schedule assumes for its balance (not for correctness).
+    const int64_t items = (int64_t)p.num_seqs * p.units;
+    const int64_t grid = (int64_t)device_cus() * per_cu;
+    if (grid > 0 && items >= 2 * grid) {
+      hipLaunchKernelGGL((paged_decode_persist_kernel<QT, CT, D, BS>), dim3((unsigned)grid), dim3(NT), 0, stream,
+                         p);
+      return hipGetLastError();
+    }
+  }
   const int64_t nwg = (int64_t)p.max_parts * p.num_seqs * p.units;
   hipLaunchKernelGGL((paged_decode_part_kernel<QT, CT, D, BS>), dim3((unsigned)nwg), dim3(256), 0, stream, p);
   hipError_t e = hipGetLastError();

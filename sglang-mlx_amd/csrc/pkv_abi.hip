@@ -191,11 +191,9 @@ int pkv_paged_attention(void* out, const void* query, const void* key_cache, con
       (v_head_stride * 2) % 8 != 0)
     return fail(PKV_ERR_INVALID, "cache base or strides are not aligned for vector loads");
   const pkv::DecodeWorkspace w = pkv::decode_workspace_layout(num_seqs, num_heads, head_size, parts);
-  if (parts > 1) {
-    if (workspace == nullptr || workspace_bytes < w.total)
-      return fail(PKV_ERR_INVALID, "workspace is smaller than pkv_paged_attention_workspace_size()");
-    if (!aligned16(workspace)) return fail(PKV_ERR_INVALID, "workspace must be 16-byte aligned");
-  }
+  if (workspace == nullptr || workspace_bytes < w.total)
+    return fail(PKV_ERR_INVALID, "workspace is smaller than pkv_paged_attention_workspace_size()");
+  if (!aligned16(workspace)) return fail(PKV_ERR_INVALID, "workspace must be 16-byte aligned");
 
   pkv::DecodeParams p;
   char* ws = static_cast<char*>(workspace);
@@ -206,8 +204,8 @@ int pkv_paged_attention(void* out, const void* query, const void* key_cache, con
   p.block_tables = block_tables;
   p.context_lens = context_lens;
   p.alibi = alibi_slopes;
-  p.ws_ml = ws ? reinterpret_cast<float*>(ws) : nullptr;
-  p.ws_o = ws ? reinterpret_cast<float*>(ws + w.ml_bytes) : nullptr;
+  p.ws_ml = reinterpret_cast<float*>(ws);
+  p.ws_o = reinterpret_cast<float*>(ws + w.ml_bytes);
   p.num_blocks = num_blocks;
   p.q_stride = q_stride;
   p.k_block_stride = k_block_stride;
@@ -225,6 +223,7 @@ int pkv_paged_attention(void* out, const void* query, const void* key_cache, con
   p.max_seq_len = max_seq_len;
   p.partition = ps;
   p.max_parts = parts;
+  p.persistent = partition_size == 0 && max_seq_len <= pkv::kPersistMaxSeq;
 
   bool ok = true;
   hipError_t e = hipErrorInvalidValue;

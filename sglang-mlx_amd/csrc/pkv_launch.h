@@ -16,6 +16,10 @@ enum { kF32 = 0, kF16 = 1, kBF16 = 2 };
 constexpr int kMaxPartition = 1024;
 constexpr int kTile = 16;
 constexpr int kMaxParts = 65536;
+// Limits of the persistent decode kernel: longest context (its block ids sit
+// in LDS) and the most sequences it orders longest-first.
+constexpr int kPersistMaxSeq = 16384;
+constexpr int kPersistMaxOrder = 1024;
 
 struct RacParams {
   const void* key;
@@ -62,9 +66,11 @@ struct DecodeParams {
   int32_t max_seq_len;
   int32_t partition;          // tokens per partition (multiple of 16 and block_size)
   int32_t max_parts;          // ceil(max_seq_len / partition)
+  int32_t persistent;         // 1: the persistent kernel may be used (v1 semantics, short enough contexts)
 };
 
-// Scratch carve-up shared by the size query and the launcher.
+// Scratch carve-up shared by the size query and the launcher: per-partition
+// (max, sum) pairs, then per-partition outputs.
 struct DecodeWorkspace {
   size_t ml_bytes, o_bytes, total;
 };

@@ -237,10 +237,14 @@ def _reshape_and_cache(op, key, value, key_cache, value_cache, slot_mapping, fla
         raise ValueError("key_cache and value_cache must be contiguous (they are updated in place)")
     _check_index(slot_mapping)
     dev = _on_gpu(op, key, value, key_cache, value_cache, slot_mapping)
-    if key.stride()[1:] != (D, 1):
+    # Rows must be [Hkv, D]-contiguous at a stride of at least Hkv * D; a
+    # single row's stride is meaningless (views of one token may carry any).
+    if key.stride()[1:] != (D, 1) or (N > 1 and key.stride(0) < H * D):
         key = key.contiguous()
-    if value.stride()[1:] != (D, 1):
+    if value.stride()[1:] != (D, 1) or (N > 1 and value.stride(0) < H * D):
         value = value.contiguous()
+    key_stride = key.stride(0) if N > 1 else H * D
+    value_stride = value.stride(0) if N > 1 else H * D
     slots = _as_i32(slot_mapping)
     if N == 0:
         return [key_cache, value_cache]
@@ -248,7 +252,7 @@ def _reshape_and_cache(op, key, value, key_cache, value_cache, slot_mapping, fla
     with torch.cuda.device(dev):
         st = lib.pkv_reshape_and_cache(
             key.data_ptr(), value.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
-            slots.data_ptr(), N, H, D, key.stride(0), value.stride(0), layout, bs, x, num_slots,
+            slots.data_ptr(), N, H, D, key_stride, value_stride, layout, bs, x, num_slots,
             kvc, cc, _stream(dev))
     _lib.check(st)
     return [key_cache, value_cache]

@@ -1,0 +1,109 @@
+"""GPU parity of the persistent decode schedule (paged_attention_v1 with at
+least two (sequence, KV head) items per resident workgroup: 512 or more on
+MI355X).  Tolerances as elsewhere: float16 2e-3 abs / 1e-2 rel, bfloat16
+1e-2 abs / 2e-2 rel.  The schedule is static (no counters or atomics), so
+repeated calls are bit-identical, also with a split-K call in between that
+shares the workspace."""
+
+import numpy as np
+import pytest
+import torch
+
+from pkv_cases import decode_oracle, make_decode_case, tolerance
+from pkv_torch import to_f64, to_index, to_torch
+from sglang_mlx_amd import kernels
+
+pytestmark = pytest.mark.gpu
+
+
+def run(c, partition_size=None):
+    args = (to_torch(c.q, c.q_dtype), to_torch(c.k_cache, c.cache_dtype), to_torch(c.v_cache, c.cache_dtype),
+            to_index(c.block_tables), to_index(c.context_lens), c.num_kv_heads, c.scale, c.block_size,
+            c.max_seq_len, None if c.alibi is None else torch.from_numpy(c.alibi).cuda())
+    out = (kernels.paged_attention_v1(*args) if partition_size is None
+           else kernels.paged_attention_v2(*args, partition_size=partition_size))
+    torch.cuda.synchronize()
+    return out
+
+
+def check(c):
+    out = run(c)
+    a, r = tolerance(c.q_dtype, c.cache_dtype)
+    np.testing.assert_allclose(to_f64(out), decode_oracle(c), atol=a, rtol=r)
+    return out
+
+
+@pytest.mark.parametrize("D,bs", [(64, 8), (64, 16), (128, 16), (128, 32), (256, 16), (96, 8)])
+def test_head_and_block_sizes(D, bs):
+    c = make_decode_case(3000 + D + bs, B=128, Hq=8, Hkv=4, D=D, block_size=bs, ctx_lo=1, ctx_hi=400,
+                         cache_dtype="bfloat16")
+    check(c)
+
+
+@pytest.mark.parametrize("q_dtype,cache_dtype", [("float16", "float16"), ("float32", "bfloat16"),
+                                                 ("float32", "float16")])
+def test_dtype_pairs(q_dtype, cache_dtype):
+    c = make_decode_case(3100, B=128, Hq=16, Hkv=4, D=128, block_size=16, ctx_lo=1, ctx_hi=600,
+                         cache_dtype=cache_dtype, q_dtype=q_dtype)
+    check(c)
+
+
+def test_gqa7_alibi_and_zero_rows():
+    c = make_decode_case(3200, B=128, Hq=28, Hkv=4, D=128, block_size=16, ctx_lo=1, ctx_hi=900,
+                         cache_dtype="bfloat16", alibi=True, max_seq_len=800)
+    c.context_lens[::7] = 0            # empty contexts -> zero rows
+    out = check(c)                     # ctx > 800 -> zero rows as well
+    zero = (c.context_lens == 0) | (c.context_lens > 800)
+    assert zero.any() and torch.count_nonzero(out[torch.from_numpy(zero)]).item() == 0
+
+
+def test_more_sequences_than_the_ordering_limit():
+    # 1100 sequences: served in index order (no longest-first ordering).
+    c = make_decode_case(3300, B=1100, Hq=4, Hkv=1, D=64, block_size=16, ctx_lo=1, ctx_hi=200,
+                         cache_dtype="float16")
+    check(c)
+
+
+def test_masked_block_ids():
+    c = make_decode_case(3400, B=128, Hq=8, Hkv=4, D=64, block_size=16, ctx_lo=64, ctx_hi=300,
+                         cache_dtype="bfloat16")
+    nb = c.k_cache.shape[0]
+    c.block_tables[5, 1] = nb + 7      # outside the pool: its tokens are masked out
+    c.block_tables[9, 0] = -5
+    out = to_f64(run(c))
+    ref = decode_oracle_masked(c, nb)
+    a, r = tolerance(c.q_dtype, c.cache_dtype)
+    np.testing.assert_allclose(out, ref, atol=a, rtol=r)
+
+
+def decode_oracle_masked(c, nb):
+    """Oracle with the tokens of out-of-pool blocks removed."""
+    from oracle import pagedkv_oracle as orc
+    B = c.q.shape[0]
+    out = np.zeros(c.q.shape)
+    q64 = orc.decode(c.q, c.q_dtype)
+    kc, vc = orc.decode(c.k_cache, c.cache_dtype), orc.decode(c.v_cache, c.cache_dtype)
+    for s in range(B):
+        ctx = int(c.context_lens[s])
+        t = np.arange(ctx)
+        blk = c.block_tables[s][t // c.block_size]
+        keep = (blk >= 0) & (blk < nb)
+        if not keep.any():
+            continue
+        k = kc[blk[keep], :, :, (t % c.block_size)[keep], :].reshape(keep.sum(), c.num_kv_heads, -1)
+        v = vc[blk[keep], :, :, (t % c.block_size)[keep]]
+        out[s] = orc._softmax_attend(q64[s], k, v, c.scale, None)
+    return out
+
+
+def test_repeated_calls_are_bit_identical():
+    c = make_decode_case(3500, B=128, Hq=8, Hkv=4, D=128, block_size=16, ctx_lo=100, ctx_hi=2000,
+                         cache_dtype="bfloat16")
+    first = run(c)
+    outs = [run(c) for _ in range(4)]
+    run(c, partition_size=256)         # split-K call sharing the workspace in between
+    outs.append(run(c))
+    for o in outs:
+        assert torch.equal(o, first)
+    a, r = tolerance(c.q_dtype, c.cache_dtype)
+    np.testing.assert_allclose(to_f64(first), decode_oracle(c), atol=a, rtol=r)
