@@ -123,7 +123,8 @@ size_t pkv_paged_attention_workspace_size(int32_t num_seqs, int32_t num_heads,
  * longest contexts first; otherwise a partition kernel, plus a log-sum-exp
  * merge kernel when a sequence has more than one partition.
  * query   : [num_seqs, num_heads, head_size], row stride q_stride.
- * out     : [num_seqs, num_heads, head_size] contiguous, same dtype as query.
+ * out     : [num_seqs, num_heads, head_size] contiguous, same dtype as
+ *           query, 16-byte aligned.
  * block_tables: [num_seqs, max_num_blocks_per_seq]; entries past
  *               ceil(ctx / block_size) are never read.  Entries outside
  *               [0, num_blocks) mask their tokens out.

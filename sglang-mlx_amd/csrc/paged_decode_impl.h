@@ -295,8 +295,11 @@ __device__ __forceinline__ void load_query(const DecodeParams& p, int seq, int h
 // wavefront's block ids (WaveBlocks::load with the same first, NW, t0);
 // first must be wave-uniform.  Tiles that lie entirely inside the range go
 // through a prefetching loop; the one tile that crosses t1 (if any) is
-// consumed last, with masking, by the wavefront it belongs to.
-template <class QT, class CT, int D, int BS, int NW, int MAXT>
+// consumed last, with masking, by the wavefront it belongs to.  MAXBUF caps
+// the tiles a wavefront keeps in flight (the default policy's depth suits
+// few workgroups per CU; with a full CU of eight streaming wavefronts, two
+// tiles each keep the memory system just as busy).
+template <class QT, class CT, int D, int BS, int NW, int MAXT, int MAXBUF = 4>
 __device__ __forceinline__ void stream_tiles(const DecodeParams& p, const uint16_t* kbase, const uint16_t* vbase,
                                              const WaveBlocks<BS, MAXT>& blk, int t0, int t1, uint32_t ctx,
                                              int first, int g, int col, const uint4 (&qa)[Tile<D>::KSTEPS],
@@ -314,7 +317,8 @@ __device__ __forceinline__ void stream_tiles(const DecodeParams& p, const uint16
   // flight.  Waiting for the current tile's loads explicitly (instead of
   // letting each use wait) also tells the compiler that every older load has
   // landed, so reusing registers across the loop back-edge costs no drain.
-  constexpr int NBUF = Prefetch<QT, D, BS>::kBuffers;
+  constexpr int NBUF = Prefetch<QT, D, BS>::kBuffers < MAXBUF ? Prefetch<QT, D, BS>::kBuffers : MAXBUF;
+  static_assert(NBUF >= 2, "the prefetch loop needs at least two tile buffers");
   constexpr int LOADS = KSTEPS + DT;
   constexpr int AHEAD = (NBUF - 1) * LOADS;
   static_assert(AHEAD < 64, "vmcnt counts at most 63 outstanding loads");
@@ -503,6 +507,84 @@ __device__ __forceinline__ void write_output(const DecodeParams& p, int64_t hrow
     }
 }
 
+// Four consecutive output elements (16-byte aligned for float32, 8-byte
+// aligned for the half types).
+template <class QT>
+__device__ __forceinline__ void store4(typename Elem<QT>::storage* dst, float a, float b, float c, float d) {
+  if constexpr (std::is_same<QT, F32>::value) {
+    *reinterpret_cast<float4*>(dst) = make_float4(a, b, c, d);
+  } else {
+    const uint32_t lo = (uint32_t)from_f32<QT>(a) | ((uint32_t)from_f32<QT>(b) << 16);
+    const uint32_t hi = (uint32_t)from_f32<QT>(c) | ((uint32_t)from_f32<QT>(d) << 16);
+    *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
+  }
+}
+
+// Merge of the NW wavefronts' states that leaves every wavefront with an
+// equal share of the output: each wavefront moves its state onto its true
+// maximum and stores it in LDS; after one barrier, wavefront w combines
+// dimension tiles w, w+NW, ... of every head row and writes them.  (With one
+// wavefront doing all of the merge, the others would queue the next item's
+// loads ahead of its output stores and it would start that item late.)
+// The weights and sums follow the same order as merge_waves, so the result
+// is the reference's sum(exp(s - max) v) / (sum(exp(s - max)) + 1e-6).
+template <class QT, int D, int NW>
+__device__ __forceinline__ void merge_store_waves(const DecodeParams& p, WaveAcc<D>& acc,
+                                                  float4 (*s_red)[Tile<D>::DT][64], float (*s_m)[16],
+                                                  float (*s_l)[16], int wave, int lane, int g, int col, int64_t hrow0,
+                                                  int nh) {
+  using QS = typename Elem<QT>::storage;
+  constexpr int DT = Tile<D>::DT;
+  if (acc.m_max != -INFINITY && acc.m_max != acc.m_run) {
+    const float f = exp2f(acc.m_run - acc.m_max);
+    acc.l_run *= f;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) acc.o[dt] *= f;
+    acc.m_run = acc.m_max;
+  }
+  const float l_col = column_sum(acc.l_run);
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+    s_red[wave][dt][lane] = make_float4(acc.o[dt][0], acc.o[dt][1], acc.o[dt][2], acc.o[dt][3]);
+  if (g == 0) {
+    s_m[wave][col] = acc.m_run;
+    s_l[wave][col] = l_col;
+  }
+  __syncthreads();
+  if (col >= nh) return;
+  float M = s_m[0][col];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) M = fmaxf(M, s_m[w][col]);
+  const float mu = M == -INFINITY ? 0.f : M;
+  float aw[NW];
+  float L = 0.f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    aw[w] = exp2f(s_m[w][col] - mu);
+    L += s_l[w][col] * aw[w];
+  }
+  const float inv = 1.f / (L + 1e-6f);
+  QS* out = static_cast<QS*>(p.out) + (hrow0 + col) * D;
+  for (int dt = wave; dt < DT; dt += NW) {
+    const int d0 = 16 * dt + 4 * g;
+    if (D % 16 != 0 && d0 >= D) continue;  // head sizes are multiples of 8
+    float4 o = s_red[0][dt][lane];
+    o.x *= aw[0];
+    o.y *= aw[0];
+    o.z *= aw[0];
+    o.w *= aw[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) {
+      const float4 x = s_red[w][dt][lane];
+      o.x += aw[w] * x.x;
+      o.y += aw[w] * x.y;
+      o.z += aw[w] * x.z;
+      o.w += aw[w] * x.w;
+    }
+    store4<QT>(out + d0, o.x * inv, o.y * inv, o.z * inv, o.w * inv);
+  }
+}
+
 __device__ __forceinline__ void unit_heads(const DecodeParams& p, int unit, int& kvh, int& h0, int& nh) {
   kvh = unit / p.slices;
   const int slice = unit - kvh * p.slices;
@@ -618,7 +700,7 @@ __global__ __launch_bounds__(64 * Persist<D>::kWaves) void paged_decode_persist_
   constexpr bool SPLIT_Q = std::is_same<QT, F32>::value;
   constexpr int MAXT = kPersistMaxSeq / kTile / NW;  // tiles per wavefront
 
-  __shared__ float s_red[2][NW - 1][DT * 4][64];
+  __shared__ float4 s_red[2][NW][DT][64];
   __shared__ float s_m[2][NW][16];
   __shared__ float s_l[2][NW][16];
   __shared__ uint32_t s_ctx[kPersistMaxOrder];
@@ -705,14 +787,14 @@ __global__ __launch_bounds__(64 * Persist<D>::kWaves) void paged_decode_persist_
     if (it.live) {
       const uint16_t* kbase = static_cast<const uint16_t*>(p.k_cache) + (int64_t)it.kvh * p.k_head_stride;
       const uint16_t* vbase = static_cast<const uint16_t*>(p.v_cache) + (int64_t)it.kvh * p.v_head_stride;
-      stream_tiles<QT, CT, D, BS, NW, MAXT>(p, kbase, vbase, blk, 0, (int)it.ctx, it.ctx, wave, g, col, qa, qb,
-                                            slope, acc);
+      stream_tiles<QT, CT, D, BS, NW, MAXT, 2>(p, kbase, vbase, blk, 0, (int)it.ctx, it.ctx, wave, g, col, qa,
+                                               qb, slope, acc);
     }
-    float M, L;
-    // s_red[buf] is written again two items later, after the next item's
-    // barrier, which wavefront 0 reaches only once it has read it.
-    merge_waves<D, NW>(acc, s_red[buf], s_m[buf], s_l[buf], wave, lane, g, col, M, L);
-    if (wave == 0 && col < it.nh) write_output<QT, D>(p, (int64_t)it.seq * p.num_heads + it.h0 + col, acc, L, g);
+    // Every wavefront reads s_red[buf] right after this item's barrier and
+    // before it reaches the next item's; s_red[buf] is written again only
+    // after that one, two items later.
+    merge_store_waves<QT, D, NW>(p, acc, s_red[buf], s_m[buf], s_l[buf], wave, lane, g, col,
+                                 (int64_t)it.seq * p.num_heads + it.h0, it.nh);
     if (!has_next) break;
     it = nit;
     blk = nblk;

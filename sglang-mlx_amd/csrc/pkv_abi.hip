@@ -183,6 +183,7 @@ int pkv_paged_attention(void* out, const void* query, const void* key_cache, con
   if (num_seqs == 0) return PKV_OK;
   if (!out || !query || !key_cache || !value_cache || !block_tables || !context_lens)
     return fail(PKV_ERR_INVALID, "null buffer");
+  if (!aligned16(out)) return fail(PKV_ERR_INVALID, "out must be 16-byte aligned");
   const int qb = elem_bytes(q_dtype);
   if (!aligned16(query) || (q_stride * qb) % 16 != 0 || q_stride < (int64_t)num_heads * head_size)
     return fail(PKV_ERR_INVALID, "query rows must be 16-byte aligned with stride >= num_heads * head_size");

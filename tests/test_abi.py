@@ -75,6 +75,18 @@ def test_paged_attention_rejections(kw, code, msg):
     assert st == code and msg in err, (st, err)
 
 
+def test_paged_attention_rejects_misaligned_output():
+    import numpy as np
+    buf = np.zeros(64, dtype=np.uint8)
+    base = buf.ctypes.data
+    good = (base + 15) // 16 * 16
+    ptr = lambda a: ctypes.c_void_p(a)
+    kw = dict(out=ptr(good + 8), q=ptr(good), kc=ptr(good), vc=ptr(good), bt=ptr(good), ctx=ptr(good),
+              ws=ptr(good), ws_bytes=1 << 40)
+    st, err = attn(**kw)
+    assert st == _lib.PKV_ERR_INVALID and "out must be 16-byte aligned" in err, (st, err)
+
+
 def test_paged_attention_empty_batch_is_a_noop():
     assert attn(B=0)[0] == _lib.PKV_OK
 
