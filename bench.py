@@ -47,7 +47,7 @@ sys.path.insert(0, os.path.join(ROOT, "sglang-mlx_amd"))
 METRIC = "paged decode µs/step + HBM GB/s (% peak), bs64 ctx≤4k Llama-3-8B shape"
 PEAK_GBS = 8000.0  # MI355X HBM3E, published peak
 DECODE_KERNEL = "paged_decode_persist_kernel<BF16, BF16, 128, 16>"
-APPEND_KERNEL = "rac_token_major_kernel<BF16, BF16, 8, true>"
+APPEND_KERNEL = "rac_token_major_wave_kernel<BF16, BF16, 2>"
 
 
 def parse_args():

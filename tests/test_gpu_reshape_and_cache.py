@@ -112,6 +112,37 @@ def test_paged5d_shapes(block_size, head_dim):
     check_paged5d(case, 32, 2, head_dim)
 
 
+@pytest.mark.parametrize("H,D,cache_dtype", [(3, 128, "bfloat16"),   # 48 vectors: one token per workgroup
+                                             (5, 128, "bfloat16"),   # 80 vectors: ragged lanes
+                                             (32, 256, "bfloat16"),  # 1024 vectors: eight passes
+                                             (2, 128, "float32"),    # 64 float32 vectors
+                                             (7, 96, "float16")])    # 84 vectors
+def test_token_major_row_lengths(H, D, cache_dtype):
+    case = make_append_case(81 + H, N=70, H=H, D=D, num_slots=16 * 16, block_size=16,
+                            kv_dtype="float32" if cache_dtype == "float32" else cache_dtype,
+                            cache_dtype=cache_dtype)
+    check_token_major(case, H, D)
+
+
+def test_token_major_strided_source():
+    # Source rows 2*H*D apart (a slice of a wider projection output).
+    case = make_append_case(91, N=64, H=8, D=128, num_slots=32 * 16, block_size=16)
+    rng = np.random.default_rng(4)
+    kc0 = random_bits(rng, (case.num_slots, 8, 128), "bfloat16")
+    vc0 = random_bits(rng, (case.num_slots, 8, 128), "bfloat16")
+    rk, rv = orc.reshape_and_cache_token_major(case.key, case.value, kc0, vc0, case.slot_mapping,
+                                               "bfloat16", "bfloat16")
+    wide_k = torch.zeros((64, 16, 128), dtype=torch.bfloat16, device="cuda")
+    wide_v = torch.zeros_like(wide_k)
+    wide_k[:, :8] = to_torch(case.key, "bfloat16")
+    wide_v[:, :8] = to_torch(case.value, "bfloat16")
+    kc, vc = to_torch(kc0, "bfloat16"), to_torch(vc0, "bfloat16")
+    _ext.reshape_and_cache(wide_k[:, :8], wide_v[:, :8], kc, vc, to_index(case.slot_mapping))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(to_numpy(kc), rk)
+    np.testing.assert_array_equal(to_numpy(vc), rv)
+
+
 def test_flash_layout_4d():
     case = make_append_case(41, N=200, H=8, D=64, num_slots=64 * 16, block_size=16)
     check_token_major(case, 8, 64, flash_blocks=64)
