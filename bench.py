@@ -22,10 +22,13 @@ Printed: ONE JSON line with the driver's fields plus
                 bf16 into 65,536 slots with 5% padding, timed as a HIP graph
                 of back-to-back launches over rotating sources and pools, for
                 the token-major (MHATokenPool) and paged 5-D layouts;
+  split_k       long-context decode (Qwen2-7B shape, B 1 and 4, contexts of
+                32K/64K/128K tokens) through paged_attention_v1 and
+                paged_attention_v2 with 512-token partitions, HIP graphs;
   cpu_baseline  the reference's gather + SDPA decode restated in torch on
                 this host's cores, on the same inputs (full batch, one layer).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-append] [--no-splitk]
 """
 
 from __future__ import annotations
@@ -59,7 +62,8 @@ def parse_args():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-append", action="store_true", help="skip the append measurement")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of timed CPU baseline work")
-    ap.add_argument("--only", choices=["decode", "append", "copy"],
+    ap.add_argument("--no-splitk", action="store_true", help="skip the long-context split-K measurement")
+    ap.add_argument("--only", choices=["decode", "append", "copy", "splitk"],
                     help="run one leg and print its own short JSON line (for counter collection under "
                          "rocprofv3 --pmc): the decode layer, the token-major append, or a plain 1 GiB device "
                          "copy whose FETCH_SIZE / WRITE_SIZE calibrate the counters")
@@ -256,6 +260,44 @@ def bench_append(dev, kernels, sources: int = 24, pools: int = 4, launches: int 
     return out
 
 
+def bench_splitk(dev, kernels, launches: int = 24):
+    """Long-context split-K decode: Qwen2-7B shape (28 q / 4 kv heads, D128,
+    bs16, bf16), B in {1, 4}, every context 32K / 64K / 128K tokens.  Each
+    configuration rotates enough KV pools to exceed 600 MB (more than the
+    Infinity Cache); paged_attention_v1 (the build's own partition choice) and
+    paged_attention_v2 with 512-token partitions are timed as HIP graphs of
+    `launches` calls (median of 5 replays)."""
+    out = []
+    Hq, Hkv, D, bs = 28, 4, 128, 16
+    scale = 1.0 / math.sqrt(D)
+    for B in (1, 4):
+        for ctx in (32768, 65536, 131072):
+            pool_bytes = int(B * ctx * Hkv * D * 2 * 2 * 1.1)
+            layers = max(2, -(-600_000_000 // pool_bytes))
+            inp = decode_inputs(1004, B=B, Hq=Hq, Hkv=Hkv, D=D, bs=bs, ctx_lo=ctx, ctx_hi=ctx, layers=layers,
+                                dev=dev)
+            nbytes = decode_bytes(inp["ctx_np"], B, Hq, Hkv, D, bs)
+            row = dict(batch=B, ctx=ctx, bytes_per_launch=nbytes, kv_pools_rotated=layers)
+            for mode in ("v1", "v2_p512"):
+                def step(i, mode=mode):
+                    kc, vc = inp["pools"][i % layers]
+                    args = (inp["q"], kc, vc, inp["bt"], inp["ctx"], Hkv, scale, bs, inp["max_seq_len"])
+                    if mode == "v1":
+                        return kernels.paged_attention_v1(*args)
+                    return kernels.paged_attention_v2(*args, partition_size=512)
+
+                ms = graph_launch_ms(step, launches)
+                gbs = nbytes / (ms * 1e-3) / 1e9
+                row[mode] = dict(us=round(ms * 1e3, 2), achieved_gbs=round(gbs, 1), frac=round(gbs / PEAK_GBS, 4))
+            out.append(row)
+            del inp
+            torch.cuda.synchronize()
+            torch.cuda.empty_cache()
+    return dict(workload="qwen2-7b split-K decode: 28 q / 4 kv heads, D128, bs16, bf16, B in {1,4}, "
+                         "ctx in {32K, 64K, 128K}", configs=out,
+                method=f"HIP graph of {launches} calls over rotated pools, median of 5 replays")
+
+
 def bench_cpu(res, budget_s):
     """CPU baseline leg: the oracle package's torch-CPU gather + SDPA, same
     inputs (layer 0), full batch."""
@@ -289,6 +331,8 @@ def only_leg(args, dev, kernels):
     elif args.only == "append":
         out = bench_append(dev, kernels)
         print(json.dumps(dict(leg="append", **out)))
+    elif args.only == "splitk":
+        print(json.dumps(dict(leg="splitk", **bench_splitk(dev, kernels))))
     else:
         n = 1 << 30
         src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
@@ -360,6 +404,8 @@ def main():
     }
     if not args.no_append:
         line["append"] = bench_append(dev, kernels)
+    if not args.no_splitk:
+        line["split_k"] = bench_splitk(dev, kernels)
     if not args.no_cpu:
         line["cpu_baseline"] = bench_cpu(res, args.cpu_budget)
     else:

@@ -45,7 +45,9 @@
 
 namespace pkv {
 
-constexpr int kWaves = 4;  // wavefronts per workgroup of the partition kernel
+// Wavefronts per workgroup of the partition kernel (8 measured slower at the
+// long-context configurations: fewer resident workgroups per CU).
+constexpr int kPartWaves = 4;
 constexpr float kLog2e = 1.4426950408889634f;
 
 __device__ __forceinline__ float wave_max(float x) {
@@ -593,20 +595,20 @@ __device__ __forceinline__ void unit_heads(const DecodeParams& p, int unit, int&
 }
 
 // ---------------------------------------------------------------------------
-// Partition kernel: one workgroup of 4 wavefronts per (partition, sequence,
+// Partition kernel: one workgroup of NW wavefronts per (partition, sequence,
 // unit).
 // ---------------------------------------------------------------------------
-template <class QT, class CT, int D, int BS>
-__global__ __launch_bounds__(256) void paged_decode_part_kernel(DecodeParams p) {
+template <class QT, class CT, int D, int BS, int NW>
+__global__ __launch_bounds__(64 * NW) void paged_decode_part_kernel(DecodeParams p) {
   using QS = typename Elem<QT>::storage;
   constexpr int KSTEPS = Tile<D>::KSTEPS;
   constexpr int DT = Tile<D>::DT;
   constexpr bool SPLIT_Q = std::is_same<QT, F32>::value;
-  constexpr int MAXT = kMaxPartition / kTile / kWaves;  // tiles per wavefront
+  constexpr int MAXT = kMaxPartition / kTile / NW;  // tiles per wavefront
 
-  __shared__ float s_red[kWaves - 1][DT * 4][64];
-  __shared__ float s_m[kWaves][16];
-  __shared__ float s_l[kWaves][16];
+  __shared__ float s_red[NW - 1][DT * 4][64];
+  __shared__ float s_m[NW][16];
+  __shared__ float s_l[NW][16];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -625,7 +627,7 @@ __global__ __launch_bounds__(256) void paged_decode_part_kernel(DecodeParams p) 
   if (ctx == 0 || ctx > (uint32_t)p.max_seq_len) {
     if (part == 0) {
       QS* out = static_cast<QS*>(p.out) + ((int64_t)seq * p.num_heads + h0) * D;
-      for (int i = tid; i < nh * D; i += 256) out[i] = from_f32<QT>(0.f);
+      for (int i = tid; i < nh * D; i += 64 * NW) out[i] = from_f32<QT>(0.f);
     }
     return;
   }
@@ -637,7 +639,7 @@ __global__ __launch_bounds__(256) void paged_decode_part_kernel(DecodeParams p) 
   const int nlb = (t1 + BS - 1) / BS - lb0;
 
   WaveBlocks<BS, MAXT> blk;
-  blk.load(p.block_tables + (int64_t)seq * p.max_blocks_per_seq, p.num_blocks, nlb, lb0, t0, wave, kWaves, lane);
+  blk.load(p.block_tables + (int64_t)seq * p.max_blocks_per_seq, p.num_blocks, nlb, lb0, t0, wave, NW, lane);
   uint4 qa[KSTEPS];
   uint4 qb[SPLIT_Q ? KSTEPS : 1];
   load_query<QT, CT, D>(p, seq, h0, nh, g, col, qa, qb);
@@ -647,10 +649,12 @@ __global__ __launch_bounds__(256) void paged_decode_part_kernel(DecodeParams p) 
   acc.init();
   const uint16_t* kbase = static_cast<const uint16_t*>(p.k_cache) + (int64_t)kvh * p.k_head_stride;
   const uint16_t* vbase = static_cast<const uint16_t*>(p.v_cache) + (int64_t)kvh * p.v_head_stride;
-  stream_tiles<QT, CT, D, BS, kWaves, MAXT>(p, kbase, vbase, blk, t0, t1, ctx, wave, g, col, qa, qb, slope, acc);
+  // Two tile buffers: fewer registers, more resident workgroups per CU
+  // (measured 1-4% faster than three or four at 32K-128K contexts).
+  stream_tiles<QT, CT, D, BS, NW, MAXT, 2>(p, kbase, vbase, blk, t0, t1, ctx, wave, g, col, qa, qb, slope, acc);
 
   float M, L;
-  merge_waves<D, kWaves>(acc, s_red, s_m, s_l, wave, lane, g, col, M, L);
+  merge_waves<D, NW>(acc, s_red, s_m, s_l, wave, lane, g, col, M, L);
   if (wave != 0 || col >= nh) return;
   const int64_t hrow = (int64_t)seq * p.num_heads + h0 + col;
   if (nparts == 1) {
@@ -811,59 +815,91 @@ __global__ __launch_bounds__(64 * Persist<D>::kWaves) void paged_decode_persist_
 }
 
 // Log-sum-exp merge of the partitions of one (sequence, query head) per
-// wavefront.  Rows whose sequence fits in one partition (or has an empty or
-// over-long context) were finished by the partition kernel.
+// workgroup.  Rows whose sequence fits in one partition (or has an empty or
+// over-long context) were finished by the partition kernel.  Wavefront w takes
+// partitions w, w+NW, ..., U of them per step with their loads issued
+// together, and keeps its own running maximum (so no separate pass finds the
+// maximum first); the wavefronts' (max, sum, output) states are combined
+// through LDS.  A row of P partitions costs about P / (NW*U) dependent memory
+// round trips.
+constexpr int kMergeWaves = 8;
+
 template <class QT, int D>
-__global__ __launch_bounds__(256) void paged_decode_reduce_kernel(DecodeParams p) {
+__global__ __launch_bounds__(64 * kMergeWaves) void paged_decode_reduce_kernel(DecodeParams p) {
   using QS = typename Elem<QT>::storage;
+  constexpr int NW = kMergeWaves;
   constexpr int NDL = (D + 63) / 64;  // dimensions per lane
+  constexpr int U = 16;
+  __shared__ float s_acc[NW][NDL * 64];
+  __shared__ float s_m[NW];
+  __shared__ float s_s[NW];
   const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * kWaves + (threadIdx.x >> 6);  // seq * Hq + head
-  if (row >= (int64_t)p.num_seqs * p.num_heads) return;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t row = blockIdx.x;  // seq * Hq + head
   const int seq = (int)(row / p.num_heads);
   const uint32_t ctx = (uint32_t)p.context_lens[seq];
   if (ctx == 0 || ctx > (uint32_t)p.max_seq_len) return;
   const int nparts = ((int)ctx + p.partition - 1) / p.partition;
   if (nparts == 1) return;
-  const float* ml = p.ws_ml + row * p.max_parts * 2;
+  const float2* ml = reinterpret_cast<const float2*>(p.ws_ml) + row * p.max_parts;
   const float* po = p.ws_o + row * p.max_parts * D;
-  float mx = -INFINITY;
-  for (int i = lane; i < nparts; i += 64) mx = fmaxf(mx, ml[2 * i]);
-  mx = wave_max(mx);
-  const float mu = mx == -INFINITY ? 0.f : mx;
+  float mw = -INFINITY, sw = 0.f;
   float acc[NDL];
 #pragma unroll
-  for (int i = 0; i < NDL; ++i) acc[i] = 0.f;
-  float sum = 0.f;
-  // Eight partitions per step, their loads issued together.
-  for (int i0 = 0; i0 < nparts; i0 += 8) {
-    float2 e[8];
-    float ov[8][NDL];
+  for (int k = 0; k < NDL; ++k) acc[k] = 0.f;
+  for (int i0 = wave; i0 < nparts; i0 += NW * U) {
+    float2 e[U];
+    float ov[U][NDL];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int i = min(i0 + u, nparts - 1);
-      e[u] = *reinterpret_cast<const float2*>(ml + 2 * i);
+    for (int u = 0; u < U; ++u) {
+      const int i = i0 + u * NW < nparts ? i0 + u * NW : i0;
+      e[u] = ml[i];
 #pragma unroll
       for (int k = 0; k < NDL; ++k) {
         const int d = lane + 64 * k;
         ov[u][k] = (D % 64 == 0 || d < D) ? po[(int64_t)i * D + d] : 0.f;
       }
     }
+    float gm = -INFINITY;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const float w = i0 + u < nparts ? e[u].y * exp2f(e[u].x - mu) : 0.f;
-      sum += w;
+    for (int u = 0; u < U; ++u)
+      if (i0 + u * NW < nparts) gm = fmaxf(gm, e[u].x);
+    if (gm > mw) {  // rescale onto the new running maximum
+      const float f = mw == -INFINITY ? 0.f : exp2f(mw - gm);
+      sw *= f;
+#pragma unroll
+      for (int k = 0; k < NDL; ++k) acc[k] *= f;
+      mw = gm;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      // A partition whose tokens were all masked has m = -inf and l = 0.
+      const float w = (i0 + u * NW < nparts && e[u].x != -INFINITY) ? e[u].y * exp2f(e[u].x - mw) : 0.f;
+      sw += w;
 #pragma unroll
       for (int k = 0; k < NDL; ++k) acc[k] += w * ov[u][k];
     }
   }
-  const float inv = 1.f / (sum + 1e-6f);
-  QS* out = static_cast<QS*>(p.out) + row * D;
 #pragma unroll
-  for (int k = 0; k < NDL; ++k) {
-    const int d = lane + 64 * k;
-    if (D % 64 == 0 || d < D) out[d] = from_f32<QT>(acc[k] * inv);
+  for (int k = 0; k < NDL; ++k) s_acc[wave][lane + 64 * k] = acc[k];
+  if (lane == 0) {
+    s_m[wave] = mw;
+    s_s[wave] = sw;
   }
+  __syncthreads();
+  const int d = threadIdx.x;
+  if (d >= D) return;
+  float M = s_m[0];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) M = fmaxf(M, s_m[w]);
+  float num = 0.f, den = 0.f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) {
+    const float f = s_m[w] == -INFINITY ? 0.f : exp2f(s_m[w] - M);
+    num += s_acc[w][d] * f;
+    den += s_s[w] * f;
+  }
+  static_cast<QS*>(p.out)[row * D + d] = from_f32<QT>(num / (den + 1e-6f));
 }
 
 // ---------------------------------------------------------------------------
@@ -909,12 +945,12 @@ static hipError_t launch_one(const DecodeParams& p, hipStream_t stream) {
     }
   }
   const int64_t nwg = (int64_t)p.max_parts * p.num_seqs * p.units;
-  hipLaunchKernelGGL((paged_decode_part_kernel<QT, CT, D, BS>), dim3((unsigned)nwg), dim3(256), 0, stream, p);
+  hipLaunchKernelGGL((paged_decode_part_kernel<QT, CT, D, BS, kPartWaves>), dim3((unsigned)nwg), dim3(64 * kPartWaves),
+                     0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.max_parts == 1) return e;
   const int64_t rows = (int64_t)p.num_seqs * p.num_heads;
-  hipLaunchKernelGGL((paged_decode_reduce_kernel<QT, D>), dim3((unsigned)((rows + kWaves - 1) / kWaves)), dim3(256),
-                     0, stream, p);
+  hipLaunchKernelGGL((paged_decode_reduce_kernel<QT, D>), dim3((unsigned)rows), dim3(64 * kMergeWaves), 0, stream, p);
   return hipGetLastError();
 }
 

@@ -41,10 +41,15 @@ int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // Partition used for the single-pass (v1) semantics: 512 tokens, halved
 // while the grid would hold fewer than 2048 workgroups, doubled while one
 // sequence would need more than kMaxParts partitions.
+// Partition size of paged_attention_v1 on the partition path: the largest
+// (at most 4096 tokens, at least 256) that still gives one workgroup per CU
+// of MI355X (256).  Measured at 32K-128K contexts, fewer and longer
+// partitions win once every CU has a workgroup: the per-workgroup start-up
+// and merge cost is then paid fewer times.
+constexpr int64_t kTargetWorkgroups = 256;
 int32_t v1_partition(int32_t num_seqs, int32_t units, int32_t max_seq_len) {
-  int32_t ps = 512;
-  while (ps > 256 && (int64_t)num_seqs * units * ceil_div(max_seq_len, ps) < 2048) ps /= 2;
-  while (ceil_div(max_seq_len, ps) > pkv::kMaxParts && ps < pkv::kMaxPartition) ps *= 2;
+  int32_t ps = pkv::kMaxPartition;
+  while (ps > 256 && (int64_t)num_seqs * units * ceil_div(max_seq_len, ps) < kTargetWorkgroups) ps /= 2;
   return ps;
 }
 
@@ -62,7 +67,7 @@ int resolve_partition(int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
   } else if (ps < 0 || ps % pkv::kTile != 0 || (block_size > 0 && ps % block_size != 0) ||
              ps > pkv::kMaxPartition) {
     return fail(PKV_ERR_INVALID,
-                "partition_size must be a positive multiple of 16 and of block_size, at most 1024");
+                "partition_size must be a positive multiple of 16 and of block_size, at most 4096");
   }
   const int64_t parts = ceil_div(max_seq_len, ps);
   if (parts > pkv::kMaxParts)

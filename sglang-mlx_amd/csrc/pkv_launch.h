@@ -13,7 +13,9 @@ enum { kF32 = 0, kF16 = 1, kBF16 = 2 };
 
 // Largest split-K partition, the tile height of the decode kernel, and the
 // most partitions one sequence may be split into.
-constexpr int kMaxPartition = 1024;
+// Largest partition (tokens) of the partition kernel, for the internal v1
+// choice and for paged_attention_v2 callers alike.
+constexpr int kMaxPartition = 4096;
 constexpr int kTile = 16;
 constexpr int kMaxParts = 65536;
 // Limits of the persistent decode kernel: longest context (its block ids sit

@@ -195,8 +195,8 @@ def paged_attention_v2(query, key_cache, value_cache, block_tables, seq_lens, nu
     tokens, merged across partitions by log-sum-exp.  Same arguments and
     result as ``paged_attention_v1`` plus ``partition_size``."""
     partition_size = int(partition_size)
-    if partition_size <= 0 or partition_size % 16 or partition_size % int(block_size) or partition_size > 1024:
-        raise ValueError("partition_size must be a positive multiple of 16 and of block_size, at most 1024")
+    if partition_size <= 0 or partition_size % 16 or partition_size % int(block_size) or partition_size > 4096:
+        raise ValueError("partition_size must be a positive multiple of 16 and of block_size, at most 4096")
     return _paged_attention("PagedAttentionV2", query, key_cache, value_cache, block_tables, seq_lens,
                             num_kv_heads, scale, block_size, max_seq_len, alibi_slopes, partition_size)
 

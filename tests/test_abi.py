@@ -65,7 +65,7 @@ def attn(**kw):
     (dict(qd=_lib.PKV_F16, cd=_lib.PKV_BF16), 2, "Unsupported query/cache dtype pair"),
     (dict(qd=_lib.PKV_F32, cd=_lib.PKV_F32), 2, "Unsupported query/cache dtype pair"),
     (dict(ps=24), 1, "partition_size must be a positive multiple of 16"),
-    (dict(ps=2048), 1, "partition_size must be a positive multiple of 16"),
+    (dict(ps=8192), 1, "partition_size must be a positive multiple of 16"),
     (dict(bs=32, max_blocks=2, ps=16), 1, "partition_size must be a positive multiple of 16 and of block_size"),
     (dict(nb=0), 1, "num_blocks must be positive"),
     (dict(), 1, "null buffer"),
@@ -94,20 +94,32 @@ def test_paged_attention_empty_batch_is_a_noop():
 def test_workspace_size_closed_form():
     lib = _lib.lib()
     align = lambda x: (x + 255) // 256 * 256
-    # Llama-3-8B decode layer: 8 KV heads, 64 seqs -> 512-token partitions,
-    # 8 of them at max_seq_len 4096.
-    parts = 8
+    # v1 partitions: the largest of 4096, 2048, ... 256 tokens that still gives
+    # 256 workgroups (seqs x units x partitions).
+    # Llama-3-8B decode layer: 64 seqs x 8 KV heads at 4096 tokens -> one
+    # 4096-token partition already gives 512 workgroups.
+    parts = 1
     assert lib.pkv_paged_attention_workspace_size(64, 32, 8, 128, 4096, 0) == \
         align(64 * 32 * parts * 2 * 4) + align(64 * 32 * parts * 128 * 4)
-    # One Qwen2-7B sequence at 32K: few units, so the v1 split shrinks to 256.
-    parts = 32768 // 256
+    # One Qwen2-7B sequence at 32K (4 units): 512-token partitions, 64 of them.
+    parts = 32768 // 512
     assert lib.pkv_paged_attention_workspace_size(1, 28, 4, 128, 32768, 0) == \
         align(28 * parts * 2 * 4) + align(28 * parts * 128 * 4)
+    # Four sequences at 128K: 4096-token partitions.
+    parts = 131072 // 4096
+    assert lib.pkv_paged_attention_workspace_size(4, 28, 4, 128, 131072, 0) == \
+        align(4 * 28 * parts * 2 * 4) + align(4 * 28 * parts * 128 * 4)
+    # A short context never goes below 256-token partitions.
+    assert lib.pkv_paged_attention_workspace_size(1, 8, 1, 64, 1000, 0) == \
+        align(8 * 4 * 2 * 4) + align(8 * 4 * 64 * 4)
     # Explicit split-K partitions.
     assert lib.pkv_paged_attention_workspace_size(4, 28, 4, 128, 131072, 512) == \
         align(4 * 28 * 256 * 2 * 4) + align(4 * 28 * 256 * 128 * 4)
+    assert lib.pkv_paged_attention_workspace_size(4, 28, 4, 128, 131072, 4096) == \
+        align(4 * 28 * 32 * 2 * 4) + align(4 * 28 * 32 * 128 * 4)
     assert lib.pkv_paged_attention_workspace_size(4, 28, 4, 128, 100, 24) == 0
     assert lib.pkv_paged_attention_workspace_size(4, 28, 3, 128, 100, 0) == 0
+    assert lib.pkv_paged_attention_workspace_size(4, 28, 4, 128, 100, 8192) == 0
 
 
 def rac(**kw):

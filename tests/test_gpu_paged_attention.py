@@ -164,7 +164,7 @@ def test_alibi():
     check(c)
 
 
-@pytest.mark.parametrize("partition_size", [16, 64, 256, 512, 1024])
+@pytest.mark.parametrize("partition_size", [16, 64, 256, 512, 1024, 2048, 4096])
 def test_split_k_partitions(partition_size):
     c = make_decode_case(500 + partition_size, B=3, Hq=28, Hkv=4, D=128, block_size=16, ctx_lo=1,
                          ctx_hi=5000, cache_dtype="bfloat16")
@@ -178,6 +178,31 @@ def test_split_k_long_context_qwen2():
                          cache_dtype="bfloat16")
     check(c, partition_size=512)
     check(c)
+
+
+def test_v1_long_context_matches_split_k():
+    # Four Qwen2-7B sequences at 64K: v1 picks 4096-token partitions (16 of
+    # them per sequence).  The merged result does not depend on how the context
+    # is partitioned, so v1 must match v2 with 512-token partitions (which the
+    # oracle pins at smaller sizes) up to float32 summation order and bf16
+    # rounding.  Inputs are generated on the GPU (537 MB of KV).
+    B, Hq, Hkv, D, bs, ctx = 4, 28, 4, 128, 16, 65536
+    g = torch.Generator(device="cuda")
+    g.manual_seed(1007)
+    nblk = ctx // bs
+    nb = B * nblk + 1
+    q = torch.randn((B, Hq, D), generator=g, device="cuda").to(torch.bfloat16)
+    kc = torch.randn((nb, Hkv, D // 8, bs, 8), generator=g, device="cuda").to(torch.bfloat16)
+    vc = torch.randn((nb, Hkv, D, bs), generator=g, device="cuda").to(torch.bfloat16)
+    perm = torch.randperm(nb - 1, generator=torch.Generator().manual_seed(1007)) + 1
+    bt = perm.reshape(B, nblk).to(torch.int32).cuda()
+    lens = torch.full((B,), ctx, dtype=torch.int32, device="cuda")
+    args = (q, kc, vc, bt, lens, Hkv, 1.0 / math.sqrt(D), bs, ctx)
+    v1 = _ext.paged_attention_v1(*args)
+    v2 = _ext.paged_attention_v2(*args, partition_size=512)
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(v1.float().cpu().numpy(), v2.float().cpu().numpy(), atol=1e-2, rtol=2e-2)
+    assert torch.isfinite(v1.float()).all()
 
 
 def test_radix_shared_prefix_tables():
