@@ -151,6 +151,31 @@ int pkv_paged_attention(void* out, const void* query, const void* key_cache,
                         int32_t q_dtype, int32_t cache_dtype, void* stream);
 
 /*
+ * Whole-block copies between paged caches.  A block is block_bytes
+ * contiguous bytes of a plane (a [num_blocks, ...] cache tensor), so every
+ * layout and dtype is the same copy.  For each (src, dst) pair of
+ * block_mapping and each plane i, block dst of dst_planes[i] receives block
+ * src of src_planes[i].
+ *   copy_blocks: pass each layer's K cache and V cache as planes that are
+ *     their own source (src_planes == dst_planes).  Replaces copy_blocks
+ *     (mlx_cache.cpp:302-346, copy_blocks.metal:9-39).
+ *   swap_blocks: one plane pair (src, dst) on the device.  Replaces
+ *     swap_blocks (mlx_cache.cpp:348-370, copy_blocks.metal:55-70); copies
+ *     between host and device memory stay with the caller.
+ * src_planes, dst_planes: host arrays of num_planes device pointers.
+ * block_mapping: device int64 [num_pairs][2]; pairs whose ids fall outside
+ *   [0, src_blocks) or [0, dst_blocks) are skipped.
+ * Pairs and planes are copied concurrently: a block that is both a source
+ * and a destination in one call gives an unspecified result, as in the
+ * reference.  Launches on `stream`; nothing is allocated.
+ */
+int pkv_copy_blocks(void* const* src_planes, void* const* dst_planes,
+                    int32_t num_planes, int64_t src_blocks,
+                    int64_t dst_blocks, int64_t block_bytes,
+                    const int64_t* block_mapping, int64_t num_pairs,
+                    void* stream);
+
+/*
  * LDS bytes available to one workgroup on a device.
  * Replaces get_max_shared_memory_per_block_device_attribute
  * (mlx_device.cpp:16-20, bindings.cpp:130-133).

@@ -28,6 +28,9 @@ reference repository):
                            reference, README.md:11-19) log-sum-exp merge of
                            per-partition (max, sum, output).
 - ``gather_kv``            the per-token gather of test_paged_attention_kernel.py:93-105
+- ``copy_blocks``, ``swap_blocks``
+                           paged_attention/metal/cache/copy_blocks.metal:9-39, :55-70;
+                           paged_attention/mlx_cache.cpp:302-370
 
 Pinning (tests/test_oracle_*.py): bf16/fp16 rounding against torch's
 conversions; the append against the element loop of the reference's own test
@@ -314,3 +317,36 @@ def token_major_to_paged5d(kt: np.ndarray, vt: np.ndarray, block_size: int, x: i
     k5 = kt.reshape(nb, block_size, H, D // x, x).transpose(0, 2, 3, 1, 4).copy()
     v4 = vt.reshape(nb, block_size, H, D).transpose(0, 2, 3, 1).copy()
     return k5, v4
+
+
+# ---------------------------------------------------------------------------
+# Block copies (paged_attention/metal/cache/copy_blocks.metal:9-39, :55-70;
+# mlx_cache.cpp:302-370): for every (src, dst) pair, block dst of the
+# destination receives block src of the source, as bytes.  The reference runs
+# the pairs concurrently, so a mapping whose sources and destinations overlap
+# has no defined result; the restatement applies pairs in order and its tests
+# use mappings without such overlaps.  Out-of-range pairs are skipped here (the
+# reference does not check them).
+# ---------------------------------------------------------------------------
+def copy_blocks(key_caches, value_caches, block_mapping):
+    """Per layer: K[dst] = K[src], V[dst] = V[src] (copy_blocks.metal:9-39)."""
+    out_k, out_v = [], []
+    m = np.asarray(block_mapping, dtype=np.int64).reshape(-1, 2)
+    for kc, vc in zip(key_caches, value_caches):
+        k, v = np.array(kc, copy=True), np.array(vc, copy=True)
+        for s, d in m:
+            if 0 <= s < k.shape[0] and 0 <= d < k.shape[0]:
+                k[d] = kc[s]
+                v[d] = vc[s]
+        out_k.append(k)
+        out_v.append(v)
+    return out_k, out_v
+
+
+def swap_blocks(src, dst, block_mapping):
+    """dst[d] = src[s] for every pair (copy_blocks.metal:55-70)."""
+    out = np.array(dst, copy=True)
+    for s, d in np.asarray(block_mapping, dtype=np.int64).reshape(-1, 2):
+        if 0 <= s < src.shape[0] and 0 <= d < out.shape[0]:
+            out[d] = src[s]
+    return out

@@ -10,6 +10,8 @@
 #include "../../include/pagedkv.h"
 #include "pkv_launch.h"
 
+#include <algorithm>
+
 namespace {
 
 thread_local std::string g_last_error;
@@ -253,6 +255,41 @@ int pkv_max_shared_memory_per_block(int32_t device_id, int64_t* out) {
   const hipError_t e = hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, device_id);
   if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute");
   *out = v;
+  return PKV_OK;
+}
+
+int pkv_copy_blocks(void* const* src_planes, void* const* dst_planes, int32_t num_planes, int64_t src_blocks,
+                    int64_t dst_blocks, int64_t block_bytes, const int64_t* block_mapping, int64_t num_pairs,
+                    void* stream) {
+  if (num_planes < 0 || num_pairs < 0 || block_bytes < 0)
+    return fail(PKV_ERR_INVALID, "num_planes, num_pairs and block_bytes must be non-negative");
+  if (num_planes == 0 || num_pairs == 0 || block_bytes == 0) return PKV_OK;
+  if (src_blocks <= 0 || dst_blocks <= 0)
+    return fail(PKV_ERR_INVALID, "src and dst must have a leading block dimension");
+  if (!src_planes || !dst_planes || !block_mapping) return fail(PKV_ERR_INVALID, "null buffer");
+  bool aligned = block_bytes % 16 == 0;
+  for (int32_t i = 0; i < num_planes; ++i) {
+    if (!src_planes[i] || !dst_planes[i]) return fail(PKV_ERR_INVALID, "null buffer");
+    aligned = aligned && aligned16(src_planes[i]) && aligned16(dst_planes[i]);
+  }
+  const int64_t max_pairs = pkv::copy_blocks_max_grid_pairs(block_bytes, aligned);
+  pkv::BlockCopyParams p;
+  p.src_blocks = src_blocks;
+  p.dst_blocks = dst_blocks;
+  p.block_bytes = block_bytes;
+  for (int32_t plane0 = 0; plane0 < num_planes; plane0 += pkv::kMaxCopyPlanes) {
+    p.num_planes = std::min<int32_t>(pkv::kMaxCopyPlanes, num_planes - plane0);
+    for (int32_t i = 0; i < p.num_planes; ++i) {
+      p.src[i] = static_cast<const char*>(src_planes[plane0 + i]);
+      p.dst[i] = static_cast<char*>(dst_planes[plane0 + i]);
+    }
+    for (int64_t pair0 = 0; pair0 < num_pairs; pair0 += max_pairs) {
+      p.mapping = block_mapping + 2 * pair0;
+      p.num_pairs = std::min<int64_t>(max_pairs, num_pairs - pair0);
+      const hipError_t e = pkv::launch_copy_blocks(p, aligned, static_cast<hipStream_t>(stream));
+      if (e != hipSuccess) return hip_fail(e, "copy_blocks launch");
+    }
+  }
   return PKV_OK;
 }
 

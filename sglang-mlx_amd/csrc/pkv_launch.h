@@ -11,10 +11,9 @@ namespace pkv {
 
 enum { kF32 = 0, kF16 = 1, kBF16 = 2 };
 
-// Largest split-K partition, the tile height of the decode kernel, and the
-// most partitions one sequence may be split into.
 // Largest partition (tokens) of the partition kernel, for the internal v1
-// choice and for paged_attention_v2 callers alike.
+// choice and for paged_attention_v2 callers alike; the tile height of the
+// decode kernels; the most partitions one sequence may be split into.
 constexpr int kMaxPartition = 4096;
 constexpr int kTile = 16;
 constexpr int kMaxParts = 65536;
@@ -78,6 +77,23 @@ struct DecodeWorkspace {
 };
 DecodeWorkspace decode_workspace_layout(int32_t num_seqs, int32_t num_heads, int32_t head_size,
                                         int32_t max_parts);
+
+// Whole-block copies (copy_blocks.hip): plane i copies block src of src[i]
+// to block dst of dst[i] for every pair of the device int64 mapping.
+constexpr int kMaxCopyPlanes = 64;
+struct BlockCopyParams {
+  const int64_t* mapping;  // [num_pairs][2] = (src block, dst block)
+  int64_t num_pairs;
+  int64_t src_blocks;      // blocks in each source plane
+  int64_t dst_blocks;      // blocks in each destination plane
+  int64_t block_bytes;
+  int32_t num_planes;      // at most kMaxCopyPlanes per launch
+  const char* src[kMaxCopyPlanes];
+  char* dst[kMaxCopyPlanes];
+};
+hipError_t launch_copy_blocks(const BlockCopyParams& p, bool aligned, hipStream_t stream);
+// Most pairs one launch can take for this block size.
+int64_t copy_blocks_max_grid_pairs(int64_t block_bytes, bool aligned);
 
 struct F32;
 struct F16;

@@ -273,30 +273,85 @@ def reshape_and_cache_flash(key, value, key_cache, value_cache, slot_mapping):
                               True)
 
 
-def copy_blocks(key_caches, value_caches, block_mapping):
-    """Copy blocks src -> dst inside every cache (mlx_cache.cpp:302-346).
-
-    Not on the append/decode path; implemented with device tensor copies.
-    """
+def _block_mapping(block_mapping) -> torch.Tensor:
     _tensor(block_mapping)
-    m = block_mapping.to(torch.int64).reshape(-1, 2)
-    for c in list(key_caches) + list(value_caches):
-        _tensor(c)
-        idx = m.to(c.device)
-        c[idx[:, 1]] = c[idx[:, 0]]
-    return list(key_caches), list(value_caches)
+    if block_mapping.dim() != 2 or block_mapping.shape[1] != 2:
+        raise ValueError("block_mapping must have shape [num_pairs, 2]")
+    _check_index(block_mapping)
+    return block_mapping
+
+
+def _copy_planes(src_planes, dst_planes, src_blocks, dst_blocks, block_bytes, mapping, dev):
+    """One pkv_copy_blocks call over planes that share block counts and size."""
+    import ctypes
+    n = len(src_planes)
+    if n == 0 or mapping.shape[0] == 0:
+        return
+    m = mapping.to(device=dev, dtype=torch.int64).contiguous()
+    src_arr = (ctypes.c_void_p * n)(*[t.data_ptr() for t in src_planes])
+    dst_arr = (ctypes.c_void_p * n)(*[t.data_ptr() for t in dst_planes])
+    with torch.cuda.device(dev):
+        st = _lib.lib().pkv_copy_blocks(src_arr, dst_arr, n, src_blocks, dst_blocks, block_bytes, m.data_ptr(),
+                                        m.shape[0], _stream(dev))
+    _lib.check(st)
+
+
+def copy_blocks(key_caches, value_caches, block_mapping):
+    """Copy whole blocks src -> dst inside every layer's K and V cache, in
+    place (mlx_cache.cpp:302-346, copy_blocks.metal:9-39); returns the two
+    lists.  Checks and messages follow mlx_cache.cpp:308-330.  Pairs are
+    copied concurrently (a block that is both a source and a destination in
+    one call gives an unspecified result, as in the reference); pairs with
+    out-of-range block ids are skipped."""
+    key_caches, value_caches = list(key_caches), list(value_caches)
+    if len(key_caches) != len(value_caches):
+        raise ValueError("key_caches and value_caches size mismatch")
+    mapping = _block_mapping(block_mapping)
+    groups = []  # runs of layers with the same (device, blocks, block bytes)
+    for kc, vc in zip(key_caches, value_caches):
+        _tensor(kc)
+        _tensor(vc)
+        if kc.dim() == 0 or vc.dim() == 0 or kc.shape[0] == 0 or vc.shape[0] == 0 or kc.shape[0] != vc.shape[0]:
+            raise ValueError("key/value caches must have matching block counts")
+        if kc.dtype != vc.dtype or kc.numel() // kc.shape[0] != vc.numel() // vc.shape[0]:
+            raise ValueError("key/value cache block layouts must match")
+        if not kc.is_contiguous() or not vc.is_contiguous():
+            raise ValueError("key/value caches must be contiguous (they are updated in place)")
+        dev = _on_gpu("CopyBlocksLayer", kc, vc)
+        key = (dev, kc.shape[0], kc.numel() // kc.shape[0] * kc.element_size())
+        if groups and groups[-1][0] == key:
+            groups[-1][1].extend((kc, vc))
+        else:
+            groups.append((key, [kc, vc]))
+    for (dev, nb, block_bytes), planes in groups:
+        _copy_planes(planes, planes, nb, nb, block_bytes, mapping, dev)
+    return key_caches, value_caches
 
 
 def swap_blocks(src, dst, block_mapping):
-    """Copy blocks of ``src`` into ``dst`` (mlx_cache.cpp:348-370); returns dst.
-
-    Not on the append/decode path; implemented with tensor copies.
-    """
+    """dst[m[:, 1]] = src[m[:, 0]] block by block (mlx_cache.cpp:348-370,
+    copy_blocks.metal:55-70); updates and returns dst.  Between two tensors on
+    one GPU this is the copy kernel; with one side in host memory (the
+    offload use) each block is one asynchronous copy on the current stream.
+    Pairs with out-of-range block ids are skipped."""
     _tensor(src)
     _tensor(dst)
-    _tensor(block_mapping)
-    m = block_mapping.to(torch.int64).reshape(-1, 2)
-    dst[m[:, 1].to(dst.device)] = src[m[:, 0].to(src.device)].to(dst.device)
+    if src.dim() == 0 or dst.dim() == 0 or src.shape[0] == 0 or dst.shape[0] == 0:
+        raise ValueError("src and dst must have a leading block dimension")
+    if src.dtype != dst.dtype or src.numel() // src.shape[0] != dst.numel() // dst.shape[0]:
+        raise ValueError("src and dst block layouts must match")
+    mapping = _block_mapping(block_mapping)
+    if not src.is_contiguous() or not dst.is_contiguous():
+        raise ValueError("src and dst must be contiguous")
+    if src.device.type == "cuda" and dst.device == src.device:
+        _copy_planes([src], [dst], src.shape[0], dst.shape[0], src.numel() // src.shape[0] * src.element_size(),
+                     mapping, src.device)
+        return dst
+    if src.device.type != "cuda" and dst.device.type != "cuda":
+        raise RuntimeError("SwapBlocks is GPU-only")
+    for s_blk, d_blk in mapping.to("cpu", torch.int64).tolist():
+        if 0 <= s_blk < src.shape[0] and 0 <= d_blk < dst.shape[0]:
+            dst[d_blk].copy_(src[s_blk], non_blocking=True)
     return dst
 
 

@@ -52,6 +52,10 @@ SIGNATURES = {
         _c_void_p, _size,                                         # workspace, bytes
         _i32, _i32, _c_void_p,                                    # q dtype, cache dtype, stream
     ]),
+    "pkv_copy_blocks": (ctypes.c_int, [
+        ctypes.POINTER(_c_void_p), ctypes.POINTER(_c_void_p), _i32,  # src/dst planes, count
+        _i64, _i64, _i64,                                            # src/dst blocks, block bytes
+        _c_void_p, _i64, _c_void_p]),                                # mapping, pairs, stream
     "pkv_max_shared_memory_per_block": (ctypes.c_int, [_i32, ctypes.POINTER(_i64)]),
     "pkv_get_device_attribute": (ctypes.c_int, [_i32, _i32, ctypes.POINTER(_i64)]),
 }
