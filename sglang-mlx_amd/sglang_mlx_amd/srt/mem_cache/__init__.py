@@ -1,5 +1,6 @@
 """KV memory management around the paged-KV kernels: slot allocator, HBM
-pool, per-request cache adapter and the radix prefix cache."""
+pool, per-request cache adapter, the radix prefix cache, and their
+block-granular counterparts for the paged kernels."""
 
 from .base_prefix_cache import (BasePrefixCache, EvictParams, EvictResult, InsertParams, InsertResult,
                                 MatchResult)
@@ -7,10 +8,11 @@ from .cache_init_params import CacheInitParams
 from .evict_policy import (EvictionStrategy, FIFOStrategy, FILOStrategy, LFUStrategy, LRUStrategy, MRUStrategy,
                            PriorityStrategy)
 from .memory_pool import MHATokenPool, PooledKVCache, TokenPoolAllocator
+from .paged_pool import BlockAllocator, BlockRadixCache, BlockTable, build_block_tables
 from .radix_cache import RadixCache, TreeNode
 
 __all__ = [
-    "BasePrefixCache", "CacheInitParams", "EvictParams", "EvictResult", "EvictionStrategy", "FIFOStrategy",
+    "BasePrefixCache", "BlockAllocator", "BlockRadixCache", "BlockTable", "build_block_tables", "CacheInitParams", "EvictParams", "EvictResult", "EvictionStrategy", "FIFOStrategy",
     "FILOStrategy", "InsertParams", "InsertResult", "LFUStrategy", "LRUStrategy", "MHATokenPool", "MRUStrategy",
     "MatchResult", "PooledKVCache", "PriorityStrategy", "RadixCache", "TokenPoolAllocator", "TreeNode",
 ]
