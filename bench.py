@@ -25,10 +25,14 @@ Printed: ONE JSON line with the driver's fields plus
   split_k       long-context decode (Qwen2-7B shape, B 1 and 4, contexts of
                 32K/64K/128K tokens) through paged_attention_v1 and
                 paged_attention_v2 with 512-token partitions, HIP graphs;
+  radix_shared  256 sequences sharing a 2048-token prefix (128 blocks) plus
+                64..512 private tokens, with 10% private-block churn through
+                the block allocator and the append kernel between steps;
+                bandwidth over unique bytes (prefix once) and logical bytes;
   cpu_baseline  the reference's gather + SDPA decode restated in torch on
                 this host's cores, on the same inputs (full batch, one layer).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-append] [--no-splitk]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-append] [--no-splitk] [--no-radix]
 """
 
 from __future__ import annotations
@@ -63,7 +67,8 @@ def parse_args():
     ap.add_argument("--no-append", action="store_true", help="skip the append measurement")
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of timed CPU baseline work")
     ap.add_argument("--no-splitk", action="store_true", help="skip the long-context split-K measurement")
-    ap.add_argument("--only", choices=["decode", "append", "copy", "splitk"],
+    ap.add_argument("--no-radix", action="store_true", help="skip the radix-shared decode measurement")
+    ap.add_argument("--only", choices=["decode", "append", "copy", "splitk", "radix"],
                     help="run one leg and print its own short JSON line (for counter collection under "
                          "rocprofv3 --pmc): the decode layer, the token-major append, or a plain 1 GiB device "
                          "copy whose FETCH_SIZE / WRITE_SIZE calibrate the counters")
@@ -298,6 +303,84 @@ def bench_splitk(dev, kernels, launches: int = 24):
                 method=f"HIP graph of {launches} calls over rotated pools, median of 5 replays")
 
 
+def bench_radix(dev, kernels, steps: int = 40, warmup: int = 5, layers: int = 2):
+    """Radix-shared decode: 256 sequences (Llama-3-8B heads: 32 q / 8 kv,
+    D128, bs16, bf16) whose block tables all start with the same 128 blocks
+    (a 2048-token shared prefix) followed by 64..512 private tokens.  Between
+    steps 10% of the private blocks are freed through the block allocator
+    (LIFO), re-allocated, their K/V rewritten with the append kernel into the
+    paged caches, and the tables rebuilt.  Each step decodes one of `layers`
+    independent layer pools (each with its own prefix blocks); the decode
+    launch alone is timed with a HIP event pair."""
+    from sglang_mlx_amd.srt.mem_cache import BlockAllocator, BlockTable, build_block_tables
+
+    B, Hq, Hkv, D, bs = 256, 32, 8, 128, 16
+    shared_blocks = 128
+    rng = np.random.default_rng(1005)
+    priv_tokens = rng.integers(64, 513, size=B)
+    nb = int((shared_blocks + (-(-priv_tokens // bs)).sum()) * 1.2) + 1
+    alloc = BlockAllocator(nb)
+    shared = alloc.alloc(shared_blocks)
+    tables = []
+    for i in range(B):
+        t = BlockTable.from_prefix(alloc, bs, shared)
+        t.append_slots(int(priv_tokens[i]), alloc)
+        tables.append(t)
+    alloc.free(shared)  # the tables hold the prefix from here on
+    max_blocks = max(len(t.blocks) for t in tables) + 1
+    g = torch.Generator(device=dev)
+    g.manual_seed(1005)
+    pools = [(torch.randn((nb, Hkv, D // 8, bs, 8), generator=g, device=dev).to(torch.bfloat16),
+              torch.randn((nb, Hkv, D, bs), generator=g, device=dev).to(torch.bfloat16)) for _ in range(layers)]
+    q = torch.randn((B, Hq, D), generator=g, device=dev).to(torch.bfloat16)
+    src_k = torch.randn((B * 32, Hkv, D), generator=g, device=dev).to(torch.bfloat16)
+    src_v = torch.randn((B * 32, Hkv, D), generator=g, device=dev).to(torch.bfloat16)
+    scale = 1.0 / math.sqrt(D)
+
+    def churn():
+        """Free 10% of the private blocks, re-allocate, rewrite their tokens."""
+        private = [(i, j) for i, t in enumerate(tables) for j in range(shared_blocks, len(t.blocks))]
+        pick = rng.choice(len(private), size=len(private) // 10, replace=False)
+        victims = [private[k] for k in pick]
+        alloc.free([tables[i].blocks[j] for i, j in victims])
+        fresh = alloc.alloc(len(victims))
+        slots = []
+        for (i, j), blk in zip(victims, fresh):
+            tables[i].blocks[j] = blk
+            ntok = min(bs, tables[i].num_tokens - j * bs)
+            slots.extend(blk * bs + o for o in range(ntok))
+        slots = torch.tensor(slots, dtype=torch.int32).to(dev, non_blocking=True)
+        n = slots.shape[0]
+        for kc, vc in pools:
+            kernels.reshape_and_cache(src_k[:n], src_v[:n], kc, vc, slots)
+        bt, ctx = build_block_tables(tables, max_blocks)
+        return torch.from_numpy(bt).to(dev, non_blocking=True), torch.from_numpy(ctx).to(dev, non_blocking=True)
+
+    times = []
+    for it in range(warmup + steps):
+        bt, ctx = churn()
+        kc, vc = pools[it % layers]
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        kernels.paged_attention_v1(q, kc, vc, bt, ctx, Hkv, scale, bs, max_blocks * bs)
+        b.record()
+        if it >= warmup:
+            times.append((a, b))
+    torch.cuda.synchronize()
+    us = sorted(a.elapsed_time(b) * 1e3 for a, b in times)
+    med = us[len(us) // 2]
+    ctx_np = np.array([t.num_tokens for t in tables], dtype=np.int64)
+    logical = decode_bytes(ctx_np, B, Hq, Hkv, D, bs)
+    unique = logical - (B - 1) * shared_blocks * bs * Hkv * D * 2 * 2
+    return dict(workload="radix-shared decode: B256, 32 q / 8 kv heads, D128, bs16, bf16, 128 shared blocks "
+                         "(2048 tokens) + U[64,512] private tokens, 10% private-block evict/realloc churn per step",
+                us_per_launch=round(med, 2), unique_bytes_per_launch=int(unique), logical_bytes_per_launch=int(logical),
+                unique_gbs=round(unique / (med * 1e-6) / 1e9, 1),
+                unique_frac=round(unique / (med * 1e-6) / 1e9 / PEAK_GBS, 4),
+                effective_gbs=round(logical / (med * 1e-6) / 1e9, 1), kv_pools_rotated=layers,
+                method=f"median of {steps} decode launches, HIP events around each; churn and append outside")
+
+
 def bench_cpu(res, budget_s):
     """CPU baseline leg: the oracle package's torch-CPU gather + SDPA, same
     inputs (layer 0), full batch."""
@@ -333,6 +416,8 @@ def only_leg(args, dev, kernels):
         print(json.dumps(dict(leg="append", **out)))
     elif args.only == "splitk":
         print(json.dumps(dict(leg="splitk", **bench_splitk(dev, kernels))))
+    elif args.only == "radix":
+        print(json.dumps(dict(leg="radix", **bench_radix(dev, kernels))))
     else:
         n = 1 << 30
         src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
@@ -406,6 +491,8 @@ def main():
         line["append"] = bench_append(dev, kernels)
     if not args.no_splitk:
         line["split_k"] = bench_splitk(dev, kernels)
+    if not args.no_radix:
+        line["radix_shared"] = bench_radix(dev, kernels)
     if not args.no_cpu:
         line["cpu_baseline"] = bench_cpu(res, args.cpu_budget)
     else:
