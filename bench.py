@@ -29,10 +29,14 @@ Printed: ONE JSON line with the driver's fields plus
                 64..512 private tokens, with 10% private-block churn through
                 the block allocator and the append kernel between steps;
                 bandwidth over unique bytes (prefix once) and logical bytes;
+  token_rows    the decode layer on token-row caches: MHATokenPool's
+                [rows, Hkv, D] buffer through slot tables (block size 1) and
+                the flash layout [blocks, 16, Hkv, D];
   cpu_baseline  the reference's gather + SDPA decode restated in torch on
                 this host's cores, on the same inputs (full batch, one layer).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-append] [--no-splitk] [--no-radix]
+                       [--no-rows] [--only LEG]
 """
 
 from __future__ import annotations
@@ -68,7 +72,8 @@ def parse_args():
     ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of timed CPU baseline work")
     ap.add_argument("--no-splitk", action="store_true", help="skip the long-context split-K measurement")
     ap.add_argument("--no-radix", action="store_true", help="skip the radix-shared decode measurement")
-    ap.add_argument("--only", choices=["decode", "append", "copy", "splitk", "radix"],
+    ap.add_argument("--no-rows", action="store_true", help="skip the token-row (MHATokenPool) decode measurement")
+    ap.add_argument("--only", choices=["decode", "append", "copy", "splitk", "radix", "rows"],
                     help="run one leg and print its own short JSON line (for counter collection under "
                          "rocprofv3 --pmc): the decode layer, the token-major append, or a plain 1 GiB device "
                          "copy whose FETCH_SIZE / WRITE_SIZE calibrate the counters")
@@ -218,6 +223,52 @@ def bench_decode(args, dev, kernels):
     res = dict(inp=inp, scale=scale, out0=outs[0], nbytes=nbytes, ms_step=ms_step, mean_ms=mean_ms,
                median_single_ms=single[len(single) // 2], achieved=achieved)
     return res
+
+
+def bench_rows(dev, kernels, layers: int = 4, steps: int = 100, warmup: int = 10):
+    """The Llama-3-8B decode layer of bench_decode (same sequences and context
+    lengths) on token-row caches: MHATokenPool's [rows, 8, 128] buffer read
+    through one slot per token (block size 1; slots a seeded permutation of a
+    pool of 1.1x the tokens), and the flash layout [blocks, 16, 8, 128] through
+    the same block tables shape as the paged leg.  Layer pools rotated."""
+    B, Hq, Hkv, D = 64, 32, 8, 128
+    rng = np.random.default_rng(1003)
+    ctx = rng.integers(512, 4096 + 1, size=B).astype(np.int64)
+    g = torch.Generator(device=dev)
+    g.manual_seed(1003)
+    q = torch.randn((B, Hq, D), generator=g, device=dev).to(torch.bfloat16)
+    lens = torch.from_numpy(ctx.astype(np.int32)).to(dev)
+    scale = 1.0 / math.sqrt(D)
+    out = {}
+    for bs in (1, 16):
+        nblk = -(-ctx // bs)
+        nb = int(math.ceil(int(nblk.sum()) * 1.1)) + 1
+        perm = rng.permutation(np.arange(1, nb))
+        bt = np.full((B, -(-4096 // bs)), -1, dtype=np.int32)
+        pos = 0
+        for s in range(B):
+            bt[s, :nblk[s]] = perm[pos:pos + nblk[s]]
+            pos += nblk[s]
+        shape = (nb, Hkv, D) if bs == 1 else (nb, bs, Hkv, D)
+        pools = [(torch.randn(shape, generator=g, device=dev).to(torch.bfloat16),
+                  torch.randn(shape, generator=g, device=dev).to(torch.bfloat16)) for _ in range(layers)]
+        btd = torch.from_numpy(bt).to(dev)
+
+        def step(i, pools=pools, btd=btd, bs=bs):
+            kc, vc = pools[i % len(pools)]
+            kernels.paged_attention_v1(q, kc, vc, btd, lens, Hkv, scale, bs, 4096)
+
+        _, dev_s = timed_launches(step, steps, warmup)
+        us = dev_s * 1e6 / steps
+        nbytes = decode_bytes(ctx, B, Hq, Hkv, D, bs)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out["slot_table_bs1" if bs == 1 else "flash_bs16"] = dict(
+            us=round(us, 2), bytes_per_launch=nbytes, gbs=round(gbs, 1), frac=round(gbs / PEAK_GBS, 4))
+        del pools
+        torch.cuda.empty_cache()
+    out["kernel"] = "paged_decode_persist_kernel<BF16, BF16, 128, 0> (token-row mode)"
+    out["timing"] = f"HIP events around {steps} back-to-back launches after {warmup} warm-up launches"
+    return out
 
 
 def bench_append(dev, kernels, sources: int = 24, pools: int = 4, launches: int = 96):
@@ -418,6 +469,8 @@ def only_leg(args, dev, kernels):
         print(json.dumps(dict(leg="splitk", **bench_splitk(dev, kernels))))
     elif args.only == "radix":
         print(json.dumps(dict(leg="radix", **bench_radix(dev, kernels))))
+    elif args.only == "rows":
+        print(json.dumps(dict(leg="rows", **bench_rows(dev, kernels))))
     else:
         n = 1 << 30
         src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
@@ -493,6 +546,8 @@ def main():
         line["split_k"] = bench_splitk(dev, kernels)
     if not args.no_radix:
         line["radix_shared"] = bench_radix(dev, kernels)
+    if not args.no_rows:
+        line["token_rows"] = bench_rows(dev, kernels)
     if not args.no_cpu:
         line["cpu_baseline"] = bench_cpu(res, args.cpu_budget)
     else:

@@ -129,12 +129,26 @@ size_t pkv_paged_attention_workspace_size(int32_t num_seqs, int32_t num_heads,
  *               ceil(ctx / block_size) are never read.  Entries outside
  *               [0, num_blocks) mask their tokens out.
  * alibi_slopes: [num_heads] float32 or NULL.
- * Cache strides: k_block_stride/k_head_stride (and v_*) are the strides of
- *               the block and head dimensions (PAGED5D).  TOKEN_MAJOR is not
- *               accepted by this entry point yet (PKV_ERR_UNSUPPORTED).
+ * Cache layouts and strides (elements):
+ *   PAGED5D     K [num_blocks, Hkv, D/x, block_size, x], V [num_blocks, Hkv,
+ *               D, block_size]; k_block_stride/k_head_stride (and v_*) are
+ *               the strides of the block and head dimensions.
+ *   TOKEN_MAJOR K and V [num_blocks, block_size, Hkv, D] (the flash layout;
+ *               block_size 1 is MHATokenPool's [rows, Hkv, D] with the
+ *               block table holding slots).  k_block_stride is the stride
+ *               between blocks and a multiple of block_size; the rows of a
+ *               block are k_block_stride / block_size apart, and each must
+ *               hold (Hkv - 1) * k_head_stride + D elements, k_head_stride
+ *               >= D being the head offset inside a row; the D elements of
+ *               one head are contiguous (likewise v_*).  block_size may
+ *               also be 1.  The persistent path covers max_seq_len up to
+ *               4096 here (2048 for head sizes above 128; 16384 for
+ *               PAGED5D).
+ *               (The reference decodes the paged layout only; this is the
+ *               gather-free path its pool asks for, memory_pool.py:110-112.)
  * (q_dtype, cache_dtype): (BF16,BF16), (F16,F16), (F32,BF16), (F32,F16).
  * head_size in {32,64,80,96,112,120,128,192,256}; block_size in {8,16,32}
- * (isValidConfig, mlx_paged_attention.cpp:52-59).
+ * (isValidConfig, mlx_paged_attention.cpp:52-59), or 1 with TOKEN_MAJOR.
  */
 int pkv_paged_attention(void* out, const void* query, const void* key_cache,
                         const void* value_cache, const int32_t* block_tables,

@@ -196,6 +196,220 @@ __device__ __forceinline__ void load_tile(Tile<D>& t, const uint16_t* kbase, con
   }
 }
 
+// ---------------------------------------------------------------------------
+// Token-row layout (MHATokenPool [rows, Hkv, D] and the flash layout
+// [blocks, block_size, Hkv, D]): a token's K and V rows of one head are D
+// contiguous elements at its row, row_stride elements apart from the next
+// row.  rows[i] is the row of tile token i (-1: masked out).
+//
+// K needs no reshaping: lane (g, col) reads dimensions 32j + 8g .. +8 of
+// token col, exactly the chunks the paged layout gives it.  The PV operand
+// wants tokens 4g .. 4g+3 of one dimension in each lane, i.e. four rows per
+// lane: lanes instead load 8 consecutive dimensions of one token (lane
+// (g, 4a + i): token 4g + i, 16 bytes) and 4x4 transposes inside each quad
+// of lanes (DPP moves, no LDS) turn each half into an operand tile; which
+// dimension each operand row then stands for is tile_dim's business.  Each
+// load instruction reads 64 contiguous bytes of each of 16 rows (8-byte loads
+// read 32), which halves the V requests per tile.
+// ---------------------------------------------------------------------------
+
+// Quad transpose of 16-bit elements: lane i of a quad holds row i of a 4x4
+// matrix as (x: elements 0, 1; y: elements 2, 3); on return lane j holds
+// column j in the same form.  `sel` is quad_transpose_sel(i).
+//
+// Step 1 trades halves with lane i^2: lanes 0, 1 keep x and take the partner's
+// x, lanes 2, 3 take the partner's y and keep y, so that lane i holds
+// (P, Q) = rows (i&1, (i&1)+2) of columns 0,1 (lanes 0, 1) or 2,3 (lanes
+// 2, 3).  Step 2 interleaves 16-bit halves with lane i^1 through v_perm.
+// Every DPP move reads a register as loaded or as produced by the previous
+// step's selects, never a select of its own step's inputs: the form
+// select -> DPP -> select over the same values was miscompiled (a select's
+// input overwritten before its last use) by the ROCm 7.2 compiler.
+__device__ __forceinline__ uint32_t quad_transpose_sel(int i) {
+  // v_perm byte selectors over {S0 = partner, S1 = own}: bytes 0-3 are own,
+  // 4-7 the partner's.  Even lanes: (own.lo, partner.lo); odd lanes:
+  // (partner.hi, own.hi).
+  return (i & 1) ? 0x03020706u : 0x05040100u;
+}
+
+__device__ __forceinline__ uint2 quad_transpose16(uint2 r, int i, uint32_t sel) {
+  // quad_perm selectors: [2,3,0,1] reads lane i^2, [1,0,3,2] lane i^1.
+  constexpr int kSwap2 = 2 | (3 << 2) | (0 << 4) | (1 << 6);
+  constexpr int kSwap1 = 1 | (0 << 2) | (3 << 4) | (2 << 6);
+  const uint32_t ax = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)r.x, kSwap2, 0xf, 0xf, false);
+  const uint32_t ay = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)r.y, kSwap2, 0xf, 0xf, false);
+  const bool low = i < 2;
+  const uint32_t P = low ? r.x : ay;
+  const uint32_t Q = low ? ax : r.y;
+  const uint32_t Pp = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)P, kSwap1, 0xf, 0xf, false);
+  const uint32_t Qp = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)Q, kSwap1, 0xf, 0xf, false);
+  return make_uint2(__builtin_amdgcn_perm(Pp, P, sel), __builtin_amdgcn_perm(Qp, Q, sel));
+}
+
+// First of the four consecutive head dimensions that rows 4g .. 4g+3 of PV
+// dimension tile dt (and so acc.o[dt] of row group g) stand for.  Paged
+// layout: tile dt is dimensions 16dt .. 16dt+15 in order.  Token rows load 8
+// dimensions of one token per lane, so tiles pair up: tiles 2e and 2e+1 hold
+// 32e + 8q + {0..3} and 32e + 8q + {4..7} in row group q; an odd last tile
+// (head sizes 80, 112) is loaded and ordered as in the paged layout.
+template <int D, bool ROWS> __device__ __forceinline__ constexpr int tile_dim(int dt, int g) {
+  if constexpr (ROWS) {
+    if (dt < Tile<D>::DT / 2 * 2) return 32 * (dt >> 1) + 8 * g + 4 * (dt & 1);
+  }
+  return 16 * dt + 4 * g;
+}
+
+// rk: row of token col (the lane's K token); rv: row of token 4g + (col & 3)
+// (the lane's V token).  V: lane (g, 4a + i) loads dimensions 32e + 8a .. +7
+// of token 4g + i into tiles 2e (first four) and 2e + 1 (last four), see
+// tile_dim; an odd last tile takes dimensions 16dt + 4a .. +3.
+template <int D>
+__device__ __forceinline__ void load_tile_rows(Tile<D>& t, const uint16_t* kbase, const uint16_t* vbase,
+                                               int64_t k_row_stride, int64_t v_row_stride, int rk, int rv,
+                                               int g, int col) {
+  constexpr int NCHUNK = D / 8;  // 16-byte K chunks per token
+  t.kpb = rk;
+  t.vpb = 0;  // V validity follows the K rows (same token rows)
+  const uint16_t* kp = kbase + (int64_t)(rk < 0 ? 0 : rk) * k_row_stride;
+  const uint16_t* vp = vbase + (int64_t)(rv < 0 ? 0 : rv) * v_row_stride;
+#pragma unroll
+  for (int j = 0; j < Tile<D>::KSTEPS; ++j) {
+    const int c = 4 * j + g;
+    t.k[j] = (NCHUNK % 4 == 0 || c < NCHUNK) ? *reinterpret_cast<const uint4*>(kp + c * 8) : make_uint4(0, 0, 0, 0);
+  }
+  constexpr int PAIRS = Tile<D>::DT / 2;
+#pragma unroll
+  for (int e = 0; e < PAIRS; ++e) {
+    const int d = 32 * e + 8 * (col >> 2);
+    const uint4 x = (D % 32 == 0 || d < D) ? *reinterpret_cast<const uint4*>(vp + d) : make_uint4(0, 0, 0, 0);
+    t.v[2 * e] = make_uint2(x.x, x.y);
+    t.v[2 * e + 1] = make_uint2(x.z, x.w);
+  }
+  if constexpr (Tile<D>::DT % 2 == 1) {
+    constexpr int dt = Tile<D>::DT - 1;
+    const int d = 16 * dt + 4 * (col >> 2);
+    t.v[dt] = d < D ? *reinterpret_cast<const uint2*>(vp + d) : make_uint2(0, 0);
+  }
+}
+
+// load_tile_rows through buffer resources with 32-bit byte offsets (the
+// persistent kernel's form; k_bytes/v_bytes bound the reachable range):
+// one VGPR per address and no 64-bit arithmetic per tile.
+template <int D>
+__device__ __forceinline__ void load_tile_rows_buf(Tile<D>& t, __amdgpu_buffer_rsrc_t kr, __amdgpu_buffer_rsrc_t vr,
+                                                   uint32_t k_row_bytes, uint32_t v_row_bytes, int rk, int rv, int g,
+                                                   int col) {
+  constexpr int NCHUNK = D / 8;
+  t.kpb = rk;
+  t.vpb = 0;
+  // The products stay 32-bit (v_mul_lo_u32): folded with the add below the
+  // compiler would use v_mad_u64_u32, whose 64-bit result pair is one more
+  // live register pair per tile.
+  uint32_t ko = (uint32_t)(rk < 0 ? 0 : rk) * k_row_bytes;
+  uint32_t vo = (uint32_t)(rv < 0 ? 0 : rv) * v_row_bytes;
+  asm volatile("" : "+v"(ko), "+v"(vo));
+  ko += (uint32_t)g * 16u;
+  vo += (uint32_t)(col >> 2) * 16u;
+#pragma unroll
+  for (int j = 0; j < Tile<D>::KSTEPS; ++j) {
+    const int c = 4 * j + g;
+    t.k[j] = (NCHUNK % 4 == 0 || c < NCHUNK)
+                 ? __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(kr, ko + j * 64, 0, 0))
+                 : make_uint4(0, 0, 0, 0);
+  }
+  constexpr int PAIRS = Tile<D>::DT / 2;
+#pragma unroll
+  for (int e = 0; e < PAIRS; ++e) {
+    const int d = 32 * e + 8 * (col >> 2);
+    const uint4 x = (D % 32 == 0 || d < D)
+                        ? __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(vr, vo + e * 64, 0, 0))
+                        : make_uint4(0, 0, 0, 0);
+    t.v[2 * e] = make_uint2(x.x, x.y);
+    t.v[2 * e + 1] = make_uint2(x.z, x.w);
+  }
+  if constexpr (Tile<D>::DT % 2 == 1) {
+    // Dimensions 16dt + 4a .. +3: byte offset 32dt + 8a from the row.
+    constexpr int dt = Tile<D>::DT - 1;
+    const int d = 16 * dt + 4 * (col >> 2);
+    t.v[dt] = d < D ? __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(
+                                                    vr, vo - (uint32_t)(col >> 2) * 8u + dt * 32, 0, 0))
+                    : make_uint2(0, 0);
+  }
+}
+
+// Turns the V rows load_tile_rows left in t.v into the PV operand.
+template <int D> __device__ __forceinline__ void transpose_tile_rows(Tile<D>& t, int col) {
+  const uint32_t sel = quad_transpose_sel(col & 3);
+#pragma unroll
+  for (int dt = 0; dt < Tile<D>::DT; ++dt) t.v[dt] = quad_transpose16(t.v[dt], col & 3, sel);
+}
+
+// Row ids of a tile's tokens for the token-row layout, staged in LDS by the
+// workgroup (rows[i]: token i of the range, -1 masked).  at() returns the
+// lane's (K row, V row) for tile `tile`.
+struct LdsRows {
+  const int32_t* rows;
+  template <int D>
+  __device__ __forceinline__ void load_tile(Tile<D>& t, const DecodeParams& p, const uint16_t* kbase,
+                                            const uint16_t* vbase, int tile, int /*k*/, int g, int col) const {
+    const int32_t* r = rows + tile * kTile;
+    load_tile_rows<D>(t, kbase, vbase, p.k_block_stride, p.v_block_stride, r[col], r[4 * g + (col & 3)], g, col);
+  }
+};
+
+// Row ids of the tiles one wavefront streams, held in registers: entry
+// e = 64 * c + lane of array c is token e % 16 of the wavefront's tile number
+// e / 16 (0-based in the order the wavefront takes them), so one VGPR holds
+// four tiles and a tile's ids reach the lanes that need them through two
+// lane permutes.  Ids outside the cache (block ids outside [0, num_blocks))
+// are -1.
+template <int MAXT> struct WaveRows {
+  static constexpr int N = (MAXT * kTile + 63) / 64;
+  int v[N];
+  // 32-bit buffer views of the item's K and V head (set with the item).
+  __amdgpu_buffer_rsrc_t kr, vr;
+
+  // Tiles first, first + nw, ... of tokens [0, bound) of the block-table
+  // row `row` (block size 1 << shift): token t lives in row
+  // bt[t >> shift] << shift | t & (block size - 1).  The loads are
+  // unconditional (tokens past the bound read its last entry) so that they
+  // issue back to back.
+  __device__ __forceinline__ void load(const int32_t* row, int shift, int64_t num_blocks, int bound, int first,
+                                       int nw, int lane) {
+    int b[N];
+#pragma unroll
+    for (int c = 0; c < N; ++c) {
+      const int e = 64 * c + lane;
+      const int t = (first + (e >> 4) * nw) * kTile + (e & 15);
+      b[c] = row[min(t, bound - 1) >> shift];
+    }
+#pragma unroll
+    for (int c = 0; c < N; ++c) {
+      const int e = 64 * c + lane;
+      const int t = (first + (e >> 4) * nw) * kTile + (e & 15);
+      const bool ok = t < bound && (int64_t)(uint32_t)b[c] < num_blocks;
+      v[c] = ok ? (b[c] << shift) + (t & ((1 << shift) - 1)) : -1;
+    }
+  }
+  template <int D>
+  __device__ __forceinline__ void load_tile(Tile<D>& t, const DecodeParams& p, const uint16_t* /*kbase*/,
+                                            const uint16_t* /*vbase*/, int /*tile*/, int k, int g, int col) const {
+    const int2 r = at(k, g, col);
+    load_tile_rows_buf<D>(t, kr, vr, (uint32_t)p.k_block_stride * 2u, (uint32_t)p.v_block_stride * 2u, r.x, r.y, g,
+                          col);
+  }
+  // (K row, V row) of the lane for the wavefront's k-th tile (wave-uniform k).
+  __device__ __forceinline__ int2 at(int k, int g, int col) const {
+    const int c = k >> 2;
+    int x = v[0];
+#pragma unroll
+    for (int i = 1; i < N; ++i)
+      if (c == i) x = v[i];
+    const int base = (k & 3) * kTile;
+    return make_int2(__shfl(x, base + col), __shfl(x, base + 4 * g + (col & 3)));
+  }
+};
+
 // Block ids of the tiles one wavefront streams, held lane-indexed in a few
 // VGPRs so that each tile's ids reach SGPRs with a v_readlane: entry e =
 // 64 * c + lane of array c is block half e % PER_TILE of the wavefront's
@@ -301,9 +515,10 @@ __device__ __forceinline__ void load_query(const DecodeParams& p, int seq, int h
 // the tiles a wavefront keeps in flight (the default policy's depth suits
 // few workgroups per CU; with a full CU of eight streaming wavefronts, two
 // tiles each keep the memory system just as busy).
-template <class QT, class CT, int D, int BS, int NW, int MAXT, int MAXBUF = 4>
+template <class QT, class CT, int D, int BS, int NW, int MAXT, int MAXBUF = 4, bool ROWS = false,
+          class Blocks = WaveBlocks<BS, MAXT>>
 __device__ __forceinline__ void stream_tiles(const DecodeParams& p, const uint16_t* kbase, const uint16_t* vbase,
-                                             const WaveBlocks<BS, MAXT>& blk, int t0, int t1, uint32_t ctx,
+                                             const Blocks& blk, int t0, int t1, uint32_t ctx,
                                              int first, int g, int col, const uint4 (&qa)[Tile<D>::KSTEPS],
                                              const uint4 (&qb)[std::is_same<QT, F32>::value ? Tile<D>::KSTEPS : 1],
                                              float slope, WaveAcc<D>& acc) {
@@ -336,16 +551,29 @@ __device__ __forceinline__ void stream_tiles(const DecodeParams& p, const uint16
   auto consume = [&](auto tail_tag, Tile<D>& t, int tt0) {
     constexpr bool TAIL = decltype(tail_tag)::value;
     const int vtok = tt0 + 4 * g;
+    if constexpr (ROWS) transpose_tile_rows<D>(t, col);
     bool zero_v = false;
     if constexpr (TAIL) {
       zero_v = true;
-    } else if constexpr (BS < kTile) {
+    } else if constexpr (ROWS || BS < kTile) {
       zero_v = !__all(t.vpb >= 0 && t.kpb >= 0);
     }
     if (zero_v) {
-      const uint32_t ok = t.vpb >= 0 ? 0xffffffffu : 0u;
-      const uint32_t m01 = ok & ((vtok + 0 < t1 ? 0x0000ffffu : 0u) | (vtok + 1 < t1 ? 0xffff0000u : 0u));
-      const uint32_t m23 = ok & ((vtok + 2 < t1 ? 0x0000ffffu : 0u) | (vtok + 3 < t1 ? 0xffff0000u : 0u));
+      uint32_t m01, m23;
+      if constexpr (ROWS) {
+        // Token rows: V tokens 4g .. 4g+3 are valid where their (shared) K
+        // row is, which lane 4g + r of this row group holds.
+        const bool v0 = vtok + 0 < t1 && __shfl(t.kpb, 4 * g + 0, 16) >= 0;
+        const bool v1 = vtok + 1 < t1 && __shfl(t.kpb, 4 * g + 1, 16) >= 0;
+        const bool v2 = vtok + 2 < t1 && __shfl(t.kpb, 4 * g + 2, 16) >= 0;
+        const bool v3 = vtok + 3 < t1 && __shfl(t.kpb, 4 * g + 3, 16) >= 0;
+        m01 = (v0 ? 0x0000ffffu : 0u) | (v1 ? 0xffff0000u : 0u);
+        m23 = (v2 ? 0x0000ffffu : 0u) | (v3 ? 0xffff0000u : 0u);
+      } else {
+        const uint32_t ok = t.vpb >= 0 ? 0xffffffffu : 0u;
+        m01 = ok & ((vtok + 0 < t1 ? 0x0000ffffu : 0u) | (vtok + 1 < t1 ? 0xffff0000u : 0u));
+        m23 = ok & ((vtok + 2 < t1 ? 0x0000ffffu : 0u) | (vtok + 3 < t1 ? 0xffff0000u : 0u));
+      }
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
         t.v[dt].x &= m01;
@@ -404,10 +632,14 @@ __device__ __forceinline__ void stream_tiles(const DecodeParams& p, const uint16
   using Full = std::integral_constant<bool, false>;
   using Tail = std::integral_constant<bool, true>;
   auto load = [&](Tile<D>& t, int tile) {
-    const int k = (tile - first) / NW;
-    const int b0 = blk.get(k * PT);
-    const int b1 = PT == 2 ? blk.get(k * PT + 1) : b0;
-    load_tile<D, BS>(t, kbase, vbase, p.k_block_stride, p.v_block_stride, b0, b1, t0 + tile * kTile, g, col);
+    if constexpr (ROWS) {
+      blk.template load_tile<D>(t, p, kbase, vbase, tile, (tile - first) / NW, g, col);
+    } else {
+      const int k = (tile - first) / NW;
+      const int b0 = blk.get(k * PT);
+      const int b1 = PT == 2 ? blk.get(k * PT + 1) : b0;
+      load_tile<D, BS>(t, kbase, vbase, p.k_block_stride, p.v_block_stride, b0, b1, t0 + tile * kTile, g, col);
+    }
   };
 
   // Full tiles: NBUF register sets, the loads of the wavefront's tile
@@ -494,7 +726,7 @@ __device__ __forceinline__ void merge_waves(WaveAcc<D>& acc, float (*s_red)[Tile
 }
 
 // Writes out[row] = o / (L + 1e-6) from wavefront 0's merged state.
-template <class QT, int D>
+template <class QT, int D, bool ROWS = false>
 __device__ __forceinline__ void write_output(const DecodeParams& p, int64_t hrow, const WaveAcc<D>& acc, float L,
                                              int g) {
   using QS = typename Elem<QT>::storage;
@@ -504,7 +736,7 @@ __device__ __forceinline__ void write_output(const DecodeParams& p, int64_t hrow
   for (int dt = 0; dt < Tile<D>::DT; ++dt)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int d = 16 * dt + 4 * g + r;
+      const int d = tile_dim<D, ROWS>(dt, g) + r;
       if (D % 16 == 0 || d < D) out[d] = from_f32<QT>(acc.o[dt][r] * inv);
     }
 }
@@ -530,7 +762,7 @@ __device__ __forceinline__ void store4(typename Elem<QT>::storage* dst, float a,
 // loads ahead of its output stores and it would start that item late.)
 // The weights and sums follow the same order as merge_waves, so the result
 // is the reference's sum(exp(s - max) v) / (sum(exp(s - max)) + 1e-6).
-template <class QT, int D, int NW>
+template <class QT, int D, int NW, bool ROWS = false>
 __device__ __forceinline__ void merge_store_waves(const DecodeParams& p, WaveAcc<D>& acc,
                                                   float4 (*s_red)[Tile<D>::DT][64], float (*s_m)[16],
                                                   float (*s_l)[16], int wave, int lane, int g, int col, int64_t hrow0,
@@ -568,7 +800,7 @@ __device__ __forceinline__ void merge_store_waves(const DecodeParams& p, WaveAcc
   const float inv = 1.f / (L + 1e-6f);
   QS* out = static_cast<QS*>(p.out) + (hrow0 + col) * D;
   for (int dt = wave; dt < DT; dt += NW) {
-    const int d0 = 16 * dt + 4 * g;
+    const int d0 = tile_dim<D, ROWS>(dt, g);
     if (D % 16 != 0 && d0 >= D) continue;  // head sizes are multiples of 8
     float4 o = s_red[0][dt][lane];
     o.x *= aw[0];
@@ -675,6 +907,97 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_part_kernel(DecodeParams
 }
 
 // ---------------------------------------------------------------------------
+// Token-row kernel: the partition kernel for the token-row layout.  The
+// workgroup first stages the rows of its partition's tokens in LDS (from the
+// block table and block size; -1 for tokens past the context or in blocks
+// outside the pool), then streams tiles that gather those rows.
+// ---------------------------------------------------------------------------
+template <class QT, class CT, int D>
+__global__ __launch_bounds__(64 * kPartWaves) void paged_decode_rows_kernel(DecodeParams p) {
+  using QS = typename Elem<QT>::storage;
+  constexpr int NW = kPartWaves;
+  constexpr int KSTEPS = Tile<D>::KSTEPS;
+  constexpr int DT = Tile<D>::DT;
+  constexpr bool SPLIT_Q = std::is_same<QT, F32>::value;
+
+  __shared__ float s_red[NW - 1][DT * 4][64];
+  __shared__ float s_m[NW][16];
+  __shared__ float s_l[NW][16];
+  __shared__ int32_t s_rows[kMaxPartition];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, col = lane & 15;
+
+  const int unit = blockIdx.x % p.units;
+  const int rest = blockIdx.x / p.units;
+  const int seq = rest % p.num_seqs;
+  const int part = rest / p.num_seqs;
+  int kvh, h0, nh;
+  unit_heads(p, unit, kvh, h0, nh);
+
+  const uint32_t ctx = (uint32_t)p.context_lens[seq];
+  if (ctx == 0 || ctx > (uint32_t)p.max_seq_len) {
+    if (part == 0) {
+      QS* out = static_cast<QS*>(p.out) + ((int64_t)seq * p.num_heads + h0) * D;
+      for (int i = tid; i < nh * D; i += 64 * NW) out[i] = from_f32<QT>(0.f);
+    }
+    return;
+  }
+  const int nparts = ((int)ctx + p.partition - 1) / p.partition;
+  if (part >= nparts) return;
+  const int t0 = part * p.partition;
+  const int t1 = min(t0 + p.partition, (int)ctx);
+
+  const int32_t* bt = p.block_tables + (int64_t)seq * p.max_blocks_per_seq;
+  const int bs = p.block_size;
+  const int span = (t1 - t0 + kTile - 1) / kTile * kTile;
+  for (int i = tid; i < span; i += 64 * NW) {
+    const int t = t0 + i;
+    int r = -1;
+    if (t < t1) {
+      const int32_t b = bt[t / bs];
+      if ((int64_t)(uint32_t)b < p.num_blocks) r = b * bs + t % bs;
+    }
+    s_rows[i] = r;
+  }
+  __syncthreads();
+
+  uint4 qa[KSTEPS];
+  uint4 qb[SPLIT_Q ? KSTEPS : 1];
+  load_query<QT, CT, D>(p, seq, h0, nh, g, col, qa, qb);
+  const float slope = (p.alibi != nullptr && col < nh) ? p.alibi[h0 + col] * kLog2e : 0.f;
+
+  WaveAcc<D> acc;
+  acc.init();
+  const uint16_t* kbase = static_cast<const uint16_t*>(p.k_cache) + (int64_t)kvh * p.k_head_stride;
+  const uint16_t* vbase = static_cast<const uint16_t*>(p.v_cache) + (int64_t)kvh * p.v_head_stride;
+  stream_tiles<QT, CT, D, kTile, NW, 1, 2, true, LdsRows>(p, kbase, vbase, LdsRows{s_rows}, t0, t1, ctx, wave, g, col,
+                                                         qa, qb, slope, acc);
+
+  float M, L;
+  merge_waves<D, NW>(acc, s_red, s_m, s_l, wave, lane, g, col, M, L);
+  if (wave != 0 || col >= nh) return;
+  const int64_t hrow = (int64_t)seq * p.num_heads + h0 + col;
+  if (nparts == 1) {
+    write_output<QT, D, true>(p, hrow, acc, L, g);
+    return;
+  }
+  const int64_t slot = hrow * p.max_parts + part;
+  const float invl = L > 0.f ? 1.f / L : 0.f;
+  float* wo = p.ws_o + slot * D;
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    const int d = tile_dim<D, true>(dt, g);
+    if (D % 16 == 0 || d < D)
+      *reinterpret_cast<float4*>(wo + d) =
+          make_float4(acc.o[dt][0] * invl, acc.o[dt][1] * invl, acc.o[dt][2] * invl, acc.o[dt][3] * invl);
+  }
+  if (g == 0) *reinterpret_cast<float2*>(p.ws_ml + slot * 2) = make_float2(M, L);
+}
+
+// ---------------------------------------------------------------------------
 // Persistent kernel: one workgroup of NW wavefronts per CU works through
 // whole (sequence, unit) items and produces their output rows without any
 // partial results.  Items are ranked longest context first and dealt in a
@@ -683,10 +1006,18 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_part_kernel(DecodeParams
 // streams one item it already loads the next item's context length, block
 // ids and query, so consecutive items follow each other without a gap.
 // ---------------------------------------------------------------------------
-template <int D> struct Persist {
+#ifndef PKV_ROWS_WAVES
+#define PKV_ROWS_WAVES 8
+#endif
+#ifndef PKV_ROWS_NBUF
+#define PKV_ROWS_NBUF 2
+#endif
+template <int D, bool ROWS = false> struct Persist {
   // Wavefronts per workgroup: two per SIMD while the register budget allows
   // (head sizes up to 128), one above.
-  static constexpr int kWaves = D <= 128 ? 8 : 4;
+  static constexpr int kWaves = D <= 128 ? (ROWS ? PKV_ROWS_WAVES : 8) : 4;
+  // Tile buffers per wavefront.
+  static constexpr int kMaxBuf = ROWS ? PKV_ROWS_NBUF : 2;
 };
 
 struct PersistItem {
@@ -695,14 +1026,19 @@ struct PersistItem {
   bool live;  // context in (0, max_seq_len]; otherwise the rows are zero
 };
 
+// BS = 0: token-row caches (any block size, p.block_size), with each
+// wavefront's row ids in registers (WaveRows); otherwise the paged layout.
 template <class QT, class CT, int D, int BS>
-__global__ __launch_bounds__(64 * Persist<D>::kWaves) void paged_decode_persist_kernel(DecodeParams p) {
-  constexpr int NW = Persist<D>::kWaves;
+__global__ __launch_bounds__(64 * (Persist<D, BS == 0>::kWaves)) void paged_decode_persist_kernel(DecodeParams p) {
+  constexpr int NW = Persist<D, BS == 0>::kWaves;
   constexpr int NT = 64 * NW;
   constexpr int KSTEPS = Tile<D>::KSTEPS;
   constexpr int DT = Tile<D>::DT;
   constexpr bool SPLIT_Q = std::is_same<QT, F32>::value;
-  constexpr int MAXT = kPersistMaxSeq / kTile / NW;  // tiles per wavefront
+  constexpr bool ROWS = BS == 0;
+  constexpr int TBS = ROWS ? kTile : BS;
+  constexpr int MAXT = (ROWS ? persist_rows_max_seq(D) : kPersistMaxSeq) / kTile / NW;  // tiles per wavefront
+  using Blocks = std::conditional_t<ROWS, WaveRows<MAXT>, WaveBlocks<TBS, MAXT>>;
 
   __shared__ float4 s_red[2][NW][DT][64];
   __shared__ float s_m[2][NW][16];
@@ -753,16 +1089,20 @@ __global__ __launch_bounds__(64 * Persist<D>::kWaves) void paged_decode_persist_
   // Block ids of the wavefront's tiles of an item.  The bound comes from
   // max_seq_len rather than the item's context, so these loads do not wait
   // for it; entries past the context are never used.
-  const int nlb_max = (p.max_seq_len + BS - 1) / BS;
-  auto load_blocks = [&](int seq, WaveBlocks<BS, MAXT>& blk) {
-    blk.load(p.block_tables + (int64_t)seq * p.max_blocks_per_seq, p.num_blocks, nlb_max, 0, 0, wave, NW, lane);
+  const int nlb_max = (p.max_seq_len + TBS - 1) / TBS;
+  auto load_blocks = [&](int seq, Blocks& blk) {
+    const int32_t* row = p.block_tables + (int64_t)seq * p.max_blocks_per_seq;
+    if constexpr (ROWS)
+      blk.load(row, __builtin_ctz((unsigned)p.block_size), p.num_blocks, p.max_seq_len, wave, NW, lane);
+    else
+      blk.load(row, p.num_blocks, nlb_max, 0, 0, wave, NW, lane);
   };
 
   int k = 0;
   const int rank = rank_of(0);
   if (rank >= total) return;
   PersistItem it = item_at(rank);
-  WaveBlocks<BS, MAXT> blk;
+  Blocks blk;
   load_blocks(it.seq, blk);
   uint4 qa[KSTEPS];
   uint4 qb[SPLIT_Q ? KSTEPS : 1];
@@ -775,7 +1115,7 @@ __global__ __launch_bounds__(64 * Persist<D>::kWaves) void paged_decode_persist_
     const int nrank = rank_of(k + 1);
     const bool has_next = nrank < total;
     PersistItem nit = it;
-    WaveBlocks<BS, MAXT> nblk;
+    Blocks nblk;
     uint4 nqa[KSTEPS];
     uint4 nqb[SPLIT_Q ? KSTEPS : 1];
     float nslope = 0.f;
@@ -791,13 +1131,18 @@ __global__ __launch_bounds__(64 * Persist<D>::kWaves) void paged_decode_persist_
     if (it.live) {
       const uint16_t* kbase = static_cast<const uint16_t*>(p.k_cache) + (int64_t)it.kvh * p.k_head_stride;
       const uint16_t* vbase = static_cast<const uint16_t*>(p.v_cache) + (int64_t)it.kvh * p.v_head_stride;
-      stream_tiles<QT, CT, D, BS, NW, MAXT, 2>(p, kbase, vbase, blk, 0, (int)it.ctx, it.ctx, wave, g, col, qa,
-                                               qb, slope, acc);
+      if constexpr (ROWS) {
+        // Every head's rows end within k_rows_bytes (v_rows_bytes) of its base.
+        blk.kr = __builtin_amdgcn_make_buffer_rsrc((void*)kbase, (short)0, (int)p.k_rows_bytes, kBufferRsrcWord3);
+        blk.vr = __builtin_amdgcn_make_buffer_rsrc((void*)vbase, (short)0, (int)p.v_rows_bytes, kBufferRsrcWord3);
+      }
+      stream_tiles<QT, CT, D, TBS, NW, MAXT, Persist<D, ROWS>::kMaxBuf, ROWS, Blocks>(p, kbase, vbase, blk, 0, (int)it.ctx, it.ctx, wave, g,
+                                                              col, qa, qb, slope, acc);
     }
     // Every wavefront reads s_red[buf] right after this item's barrier and
     // before it reaches the next item's; s_red[buf] is written again only
     // after that one, two items later.
-    merge_store_waves<QT, D, NW>(p, acc, s_red[buf], s_m[buf], s_l[buf], wave, lane, g, col,
+    merge_store_waves<QT, D, NW, ROWS>(p, acc, s_red[buf], s_m[buf], s_l[buf], wave, lane, g, col,
                                  (int64_t)it.seq * p.num_heads + it.h0, it.nh);
     if (!has_next) break;
     it = nit;
@@ -919,31 +1264,39 @@ inline int device_cus() {
   return cache[dev];
 }
 
+// Launches the persistent kernel (BS = 0: token rows) when the batch has
+// enough items for it; *launched says whether it did.
+template <class QT, class CT, int D, int BS>
+static hipError_t launch_persistent(const DecodeParams& p, hipStream_t stream, bool* launched) {
+  *launched = false;
+  if (!p.persistent) return hipSuccess;
+  constexpr int NT = 64 * Persist<D, BS == 0>::kWaves;
+  static int per_cu = -1;  // resident workgroups per CU for this instantiation
+  if (per_cu < 0) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, paged_decode_persist_kernel<QT, CT, D, BS>, NT, 0) !=
+            hipSuccess ||
+        n <= 0)
+      n = 1;
+    per_cu = n;
+  }
+  // Whole (sequence, unit) items balance well once there are at least two
+  // per resident workgroup; fewer, longer items go to the partition path.
+  // The grid never exceeds what is resident at once, which the snake
+  // schedule assumes for its balance (not for correctness).
+  const int64_t items = (int64_t)p.num_seqs * p.units;
+  const int64_t grid = (int64_t)device_cus() * per_cu;
+  if (grid <= 0 || items < 2 * grid) return hipSuccess;
+  *launched = true;
+  hipLaunchKernelGGL((paged_decode_persist_kernel<QT, CT, D, BS>), dim3((unsigned)grid), dim3(NT), 0, stream, p);
+  return hipGetLastError();
+}
+
 template <class QT, class CT, int D, int BS>
 static hipError_t launch_one(const DecodeParams& p, hipStream_t stream) {
-  if (p.persistent) {
-    constexpr int NT = 64 * Persist<D>::kWaves;
-    static int per_cu = -1;  // resident workgroups per CU for this instantiation
-    if (per_cu < 0) {
-      int n = 0;
-      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, paged_decode_persist_kernel<QT, CT, D, BS>, NT, 0) !=
-              hipSuccess ||
-          n <= 0)
-        n = 1;
-      per_cu = n;
-    }
-    // Whole (sequence, unit) items balance well once there are at least two
-    // per resident workgroup; fewer, longer items go to the partition path.
-    // The grid never exceeds what is resident at once, which the snake
-    // schedule assumes for its balance (not for correctness).
-    const int64_t items = (int64_t)p.num_seqs * p.units;
-    const int64_t grid = (int64_t)device_cus() * per_cu;
-    if (grid > 0 && items >= 2 * grid) {
-      hipLaunchKernelGGL((paged_decode_persist_kernel<QT, CT, D, BS>), dim3((unsigned)grid), dim3(NT), 0, stream,
-                         p);
-      return hipGetLastError();
-    }
-  }
+  bool launched = false;
+  const hipError_t pe = launch_persistent<QT, CT, D, BS>(p, stream, &launched);
+  if (launched || pe != hipSuccess) return pe;
   const int64_t nwg = (int64_t)p.max_parts * p.num_seqs * p.units;
   hipLaunchKernelGGL((paged_decode_part_kernel<QT, CT, D, BS, kPartWaves>), dim3((unsigned)nwg), dim3(64 * kPartWaves),
                      0, stream, p);
@@ -965,19 +1318,42 @@ static hipError_t launch_bs(const DecodeParams& p, int block_size, hipStream_t s
   return hipErrorInvalidValue;
 }
 
+// Token-row layout: the persistent kernel in its token-row mode, else the
+// token-row kernel plus the merge kernel when a sequence spans several
+// partitions.
+template <class QT, class CT, int D>
+static hipError_t launch_rows(const DecodeParams& p, hipStream_t stream) {
+  bool launched = false;
+  const hipError_t pe = launch_persistent<QT, CT, D, 0>(p, stream, &launched);
+  if (launched || pe != hipSuccess) return pe;
+  const int64_t nwg = (int64_t)p.max_parts * p.num_seqs * p.units;
+  hipLaunchKernelGGL((paged_decode_rows_kernel<QT, CT, D>), dim3((unsigned)nwg), dim3(64 * kPartWaves), 0, stream, p);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || p.max_parts == 1) return e;
+  const int64_t rows = (int64_t)p.num_seqs * p.num_heads;
+  hipLaunchKernelGGL((paged_decode_reduce_kernel<QT, D>), dim3((unsigned)rows), dim3(64 * kMergeWaves), 0, stream, p);
+  return hipGetLastError();
+}
+
+template <class QT, class CT, int D>
+static hipError_t launch_layout(const DecodeParams& p, int block_size, hipStream_t stream, bool* ok) {
+  if (p.rows) return launch_rows<QT, CT, D>(p, stream);
+  return launch_bs<QT, CT, D>(p, block_size, stream, ok);
+}
+
 template <class QT, class CT>
 hipError_t launch_decode_typed(const DecodeParams& p, int head_size, int block_size, hipStream_t stream,
                                bool* ok) {
   switch (head_size) {
-    case 32: return launch_bs<QT, CT, 32>(p, block_size, stream, ok);
-    case 64: return launch_bs<QT, CT, 64>(p, block_size, stream, ok);
-    case 80: return launch_bs<QT, CT, 80>(p, block_size, stream, ok);
-    case 96: return launch_bs<QT, CT, 96>(p, block_size, stream, ok);
-    case 112: return launch_bs<QT, CT, 112>(p, block_size, stream, ok);
-    case 120: return launch_bs<QT, CT, 120>(p, block_size, stream, ok);
-    case 128: return launch_bs<QT, CT, 128>(p, block_size, stream, ok);
-    case 192: return launch_bs<QT, CT, 192>(p, block_size, stream, ok);
-    case 256: return launch_bs<QT, CT, 256>(p, block_size, stream, ok);
+    case 32: return launch_layout<QT, CT, 32>(p, block_size, stream, ok);
+    case 64: return launch_layout<QT, CT, 64>(p, block_size, stream, ok);
+    case 80: return launch_layout<QT, CT, 80>(p, block_size, stream, ok);
+    case 96: return launch_layout<QT, CT, 96>(p, block_size, stream, ok);
+    case 112: return launch_layout<QT, CT, 112>(p, block_size, stream, ok);
+    case 120: return launch_layout<QT, CT, 120>(p, block_size, stream, ok);
+    case 128: return launch_layout<QT, CT, 128>(p, block_size, stream, ok);
+    case 192: return launch_layout<QT, CT, 192>(p, block_size, stream, ok);
+    case 256: return launch_layout<QT, CT, 256>(p, block_size, stream, ok);
   }
   *ok = false;
   return hipErrorInvalidValue;

@@ -178,10 +178,11 @@ int pkv_paged_attention(void* out, const void* query, const void* key_cache, con
   if (st != PKV_OK) return st;
   if (max_num_blocks_per_seq <= 0 || (int64_t)max_seq_len > (int64_t)max_num_blocks_per_seq * block_size)
     return fail(PKV_ERR_INVALID, "max_seq_len exceeds block table capacity");
-  if (!valid_head_size(head_size) || !valid_block_size(block_size))
+  if (layout != PKV_LAYOUT_PAGED5D && layout != PKV_LAYOUT_TOKEN_MAJOR)
+    return fail(PKV_ERR_INVALID, "Unknown cache layout");
+  const bool rows = layout == PKV_LAYOUT_TOKEN_MAJOR;
+  if (!valid_head_size(head_size) || !(valid_block_size(block_size) || (rows && block_size == 1)))
     return fail(PKV_ERR_UNSUPPORTED, "Unsupported head_size/block_size for paged_attention");
-  if (layout != PKV_LAYOUT_PAGED5D)
-    return fail(PKV_ERR_UNSUPPORTED, "paged_attention supports the paged 5-D cache layout only");
   const bool pair_ok = (q_dtype == PKV_BF16 && cache_dtype == PKV_BF16) ||
                        (q_dtype == PKV_F16 && cache_dtype == PKV_F16) ||
                        (q_dtype == PKV_F32 && (cache_dtype == PKV_BF16 || cache_dtype == PKV_F16));
@@ -194,9 +195,21 @@ int pkv_paged_attention(void* out, const void* query, const void* key_cache, con
   const int qb = elem_bytes(q_dtype);
   if (!aligned16(query) || (q_stride * qb) % 16 != 0 || q_stride < (int64_t)num_heads * head_size)
     return fail(PKV_ERR_INVALID, "query rows must be 16-byte aligned with stride >= num_heads * head_size");
-  if (!aligned16(key_cache) || (k_block_stride * 2) % 16 != 0 || (k_head_stride * 2) % 16 != 0 ||
-      (reinterpret_cast<uintptr_t>(value_cache) & 7u) != 0 || (v_block_stride * 2) % 8 != 0 ||
-      (v_head_stride * 2) % 8 != 0)
+  if (rows && (k_block_stride % block_size != 0 || v_block_stride % block_size != 0 ||
+               k_head_stride < head_size || v_head_stride < head_size ||
+               k_block_stride / block_size < (int64_t)(num_kv_heads - 1) * k_head_stride + head_size ||
+               v_block_stride / block_size < (int64_t)(num_kv_heads - 1) * v_head_stride + head_size))
+    return fail(PKV_ERR_INVALID, "token-row caches need rows that hold num_kv_heads heads of head_size");
+  if (rows && num_blocks > (int64_t)INT32_MAX / block_size)
+    return fail(PKV_ERR_UNSUPPORTED, "token-row caches hold at most 2^31 - 1 rows");
+  // Token rows: the row stride takes the place of the block stride below.
+  const int64_t kbs = rows ? k_block_stride / block_size : k_block_stride;
+  const int64_t vbs = rows ? v_block_stride / block_size : v_block_stride;
+  // V: 8-byte loads in the paged layout, 16-byte loads of token rows.
+  const int64_t v_align = rows ? 16 : 8;
+  if (!aligned16(key_cache) || (kbs * 2) % 16 != 0 || (k_head_stride * 2) % 16 != 0 ||
+      (reinterpret_cast<uintptr_t>(value_cache) % v_align) != 0 || (vbs * 2) % v_align != 0 ||
+      (v_head_stride * 2) % v_align != 0)
     return fail(PKV_ERR_INVALID, "cache base or strides are not aligned for vector loads");
   const pkv::DecodeWorkspace w = pkv::decode_workspace_layout(num_seqs, num_heads, head_size, parts);
   if (workspace == nullptr || workspace_bytes < w.total)
@@ -216,9 +229,9 @@ int pkv_paged_attention(void* out, const void* query, const void* key_cache, con
   p.ws_o = reinterpret_cast<float*>(ws + w.ml_bytes);
   p.num_blocks = num_blocks;
   p.q_stride = q_stride;
-  p.k_block_stride = k_block_stride;
+  p.k_block_stride = kbs;
   p.k_head_stride = k_head_stride;
-  p.v_block_stride = v_block_stride;
+  p.v_block_stride = vbs;
   p.v_head_stride = v_head_stride;
   p.scale_log2 = scale * 1.4426950408889634f;
   p.num_seqs = num_seqs;
@@ -231,7 +244,22 @@ int pkv_paged_attention(void* out, const void* query, const void* key_cache, con
   p.max_seq_len = max_seq_len;
   p.partition = ps;
   p.max_parts = parts;
-  p.persistent = partition_size == 0 && max_seq_len <= pkv::kPersistMaxSeq;
+  p.persistent = partition_size == 0 &&
+                 max_seq_len <= (rows ? pkv::persist_rows_max_seq(head_size) : pkv::kPersistMaxSeq);
+  p.rows = rows;
+  p.block_size = block_size;
+  p.k_rows_bytes = p.v_rows_bytes = 0;
+  if (rows) {
+    const int64_t total_rows = num_blocks * block_size;
+    const int64_t k_span = ((total_rows - 1) * kbs + head_size) * 2;
+    const int64_t v_span = ((total_rows - 1) * vbs + head_size) * 2;
+    if (k_span > (int64_t)UINT32_MAX || v_span > (int64_t)UINT32_MAX)
+      p.persistent = 0;  // 64-bit addressing: the partition kernel
+    else {
+      p.k_rows_bytes = (uint32_t)k_span;
+      p.v_rows_bytes = (uint32_t)v_span;
+    }
+  }
 
   bool ok = true;
   hipError_t e = hipErrorInvalidValue;

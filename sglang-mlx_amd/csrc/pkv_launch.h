@@ -21,6 +21,10 @@ constexpr int kMaxParts = 65536;
 // in LDS) and the most sequences it orders longest-first.
 constexpr int kPersistMaxSeq = 16384;
 constexpr int kPersistMaxOrder = 1024;
+// Token-row caches keep each wavefront's row ids in registers (8 VGPRs per
+// item), so their persistent path stops at 4096 tokens with eight wavefronts
+// per workgroup (head sizes up to 128) and at 2048 with four.
+constexpr int persist_rows_max_seq(int head_size) { return head_size > 128 ? 2048 : 4096; }
 
 struct RacParams {
   const void* key;
@@ -45,8 +49,8 @@ hipError_t launch_reshape_and_cache(const RacParams& p, bool aligned, hipStream_
 struct DecodeParams {
   void* out;                  // [B, Hq, D], query dtype
   const void* q;              // [B, Hq, D], row stride q_stride
-  const void* k_cache;        // paged 5-D K
-  const void* v_cache;        // paged 5-D V
+  const void* k_cache;        // paged 5-D K, or token rows (see rows)
+  const void* v_cache;        // paged 5-D V, or token rows
   const int32_t* block_tables;
   const int32_t* context_lens;
   const float* alibi;         // [Hq] or null
@@ -68,6 +72,18 @@ struct DecodeParams {
   int32_t partition;          // tokens per partition (multiple of 16 and block_size)
   int32_t max_parts;          // ceil(max_seq_len / partition)
   int32_t persistent;         // 1: the persistent kernel may be used (v1 semantics, short enough contexts)
+  // Token-row layout ([blocks, block_size, Hkv, D], block_size 1 being
+  // MHATokenPool's [rows, Hkv, D]): k/v_block_stride then hold the row
+  // stride (elements from one token's row to the next) and block_size the
+  // tokens per block; token t of a sequence sits at row
+  // block_tables[t / block_size] * block_size + t % block_size.
+  int32_t rows;
+  int32_t block_size;
+  // Token rows, persistent path: bytes of K and V reachable from any head's
+  // base, (rows - 1) * row bytes + head_size * element bytes; the persistent
+  // kernel addresses rows with 32-bit buffer offsets, so it is used only when
+  // both fit in 32 bits.
+  uint32_t k_rows_bytes, v_rows_bytes;
 };
 
 // Scratch carve-up shared by the size query and the launcher: per-partition

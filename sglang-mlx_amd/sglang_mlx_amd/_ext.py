@@ -94,45 +94,74 @@ def _decode_scratch(dev: torch.device, stream: int, scratch_bytes: int) -> torch
         return scratch
 
 
+def _cache_layout(key_cache, value_cache) -> int:
+    """PKV_LAYOUT_PAGED5D for K [nb, Hkv, D/x, bs, x] / V [nb, Hkv, D, bs]
+    (the reference's layout), PKV_LAYOUT_TOKEN_MAJOR for token rows: K and V
+    [rows, Hkv, D] (MHATokenPool; block size 1) or [nb, bs, Hkv, D]."""
+    if key_cache.dim() == 5 and value_cache.dim() == 4:
+        return _lib.PKV_LAYOUT_PAGED5D
+    if key_cache.dim() in (3, 4) and value_cache.dim() == key_cache.dim():
+        return _lib.PKV_LAYOUT_TOKEN_MAJOR
+    raise ValueError("key_cache/value_cache must use paged attention layouts")
+
+
 def _check_paged_attention(query, key_cache, value_cache, block_tables, context_lens,
                            num_kv_heads, block_size, max_seq_len, alibi_slopes):
-    """Checks of mlx_paged_attention.cpp:156-188, same order and messages."""
+    """Checks of mlx_paged_attention.cpp:156-188, same order and messages;
+    token-row caches (an extension) get the same checks on their own dims."""
     if query.dim() != 3:
         raise ValueError("query must have shape [num_seqs, num_heads, head_size]")
-    if key_cache.dim() != 5 or value_cache.dim() != 4:
-        raise ValueError("key_cache/value_cache must use paged attention layouts")
+    layout = _cache_layout(key_cache, value_cache)
+    rows = layout == _lib.PKV_LAYOUT_TOKEN_MAJOR
     if block_tables.dim() != 2 or context_lens.dim() != 1:
         raise ValueError("block_tables must be 2D and context_lens must be 1D")
     if query.shape[0] != block_tables.shape[0] or query.shape[0] != context_lens.shape[0]:
         raise ValueError("query, block_tables, and context_lens sequence counts differ")
     if num_kv_heads <= 0 or query.shape[1] % num_kv_heads != 0:
         raise ValueError("num_heads must be divisible by num_kv_heads")
-    if key_cache.shape[1] != num_kv_heads or value_cache.shape[1] != num_kv_heads:
-        raise ValueError("cache KV-head count does not match num_kv_heads")
-    if key_cache.shape[2] * key_cache.shape[4] != query.shape[2] or value_cache.shape[2] != query.shape[2]:
-        raise ValueError("cache head size does not match query head size")
-    if (key_cache.shape[0] != value_cache.shape[0] or key_cache.shape[3] != block_size
-            or value_cache.shape[3] != block_size):
-        raise ValueError("cache block dimensions do not match block_size")
+    if rows:
+        cache_bs = key_cache.shape[1] if key_cache.dim() == 4 else 1
+        if key_cache.shape[-2] != num_kv_heads or value_cache.shape[-2] != num_kv_heads:
+            raise ValueError("cache KV-head count does not match num_kv_heads")
+        if key_cache.shape[-1] != query.shape[2] or value_cache.shape[-1] != query.shape[2]:
+            raise ValueError("cache head size does not match query head size")
+        if key_cache.shape[:-2] != value_cache.shape[:-2] or cache_bs != block_size:
+            raise ValueError("cache block dimensions do not match block_size")
+    else:
+        if key_cache.shape[1] != num_kv_heads or value_cache.shape[1] != num_kv_heads:
+            raise ValueError("cache KV-head count does not match num_kv_heads")
+        if key_cache.shape[2] * key_cache.shape[4] != query.shape[2] or value_cache.shape[2] != query.shape[2]:
+            raise ValueError("cache head size does not match query head size")
+        if (key_cache.shape[0] != value_cache.shape[0] or key_cache.shape[3] != block_size
+                or value_cache.shape[3] != block_size):
+            raise ValueError("cache block dimensions do not match block_size")
     if alibi_slopes is not None and (alibi_slopes.dim() != 1 or alibi_slopes.shape[0] != query.shape[1]):
         raise ValueError("alibi_slopes must have shape [num_heads]")
     if max_seq_len <= 0:
         raise ValueError("max_seq_len must be positive")
     if max_seq_len > block_tables.shape[1] * block_size:
         raise ValueError("max_seq_len exceeds block table capacity")
-    if query.shape[2] not in _HEAD_SIZES or block_size not in _BLOCK_SIZES:
+    if query.shape[2] not in _HEAD_SIZES or not (block_size in _BLOCK_SIZES or (rows and block_size == 1)):
         raise ValueError("Unsupported head_size/block_size for paged_attention")
     # Checks the reference leaves to the kernel.
     qc = _dtype_code(query)
     cc = _dtype_code(key_cache)
     if value_cache.dtype != key_cache.dtype:
         raise ValueError("key_cache and value_cache dtypes differ")
-    if key_cache.shape[4] != 16 // _ELEM_BYTES[key_cache.dtype]:
+    if not rows and key_cache.shape[4] != 16 // _ELEM_BYTES[key_cache.dtype]:
         raise ValueError("key_cache last dimension must be 16 / element size of the cache dtype")
     if not (qc == cc and qc != _lib.PKV_F32) and not (qc == _lib.PKV_F32 and cc != _lib.PKV_F32):
         raise ValueError(
             f"Unsupported query/cache dtype pair for paged_attention: {query.dtype}/{key_cache.dtype}")
-    return qc, cc
+    if rows:
+        # Rows must be [Hkv, D]-contiguous, and the rows of a block evenly
+        # spaced (block stride = block_size * row stride).
+        H, D = key_cache.shape[-2], key_cache.shape[-1]
+        for name, c in (("key_cache", key_cache), ("value_cache", value_cache)):
+            if c.stride()[-2:] != (D, 1) or (c.dim() == 4 and (c.stride(1) < H * D
+                                                                or c.stride(0) != c.shape[1] * c.stride(1))):
+                raise ValueError(f"{name} rows must be contiguous [num_kv_heads, head_size]")
+    return qc, cc, layout
 
 
 def _paged_attention(op, query, key_cache, value_cache, block_tables, context_lens, num_kv_heads,
@@ -141,18 +170,19 @@ def _paged_attention(op, query, key_cache, value_cache, block_tables, context_le
         _tensor(t)
     _tensor(alibi_slopes, allow_none=True)
     num_kv_heads, block_size, max_seq_len = int(num_kv_heads), int(block_size), int(max_seq_len)
-    qc, cc = _check_paged_attention(query, key_cache, value_cache, block_tables, context_lens,
-                                    num_kv_heads, block_size, max_seq_len, alibi_slopes)
+    qc, cc, layout = _check_paged_attention(query, key_cache, value_cache, block_tables, context_lens,
+                                            num_kv_heads, block_size, max_seq_len, alibi_slopes)
     _check_index(block_tables)
     _check_index(context_lens)
     dev = _on_gpu(op, query, key_cache, value_cache, block_tables, context_lens, alibi_slopes)
     B, Hq, D = query.shape
     if query.stride(2) != 1 or query.stride(1) != D or (query.stride(0) * _ELEM_BYTES[query.dtype]) % 16:
         query = query.contiguous()
-    if key_cache.stride()[2:] != (block_size * key_cache.shape[4], key_cache.shape[4], 1):
-        key_cache = key_cache.contiguous()
-    if value_cache.stride()[2:] != (block_size, 1):
-        value_cache = value_cache.contiguous()
+    if layout == _lib.PKV_LAYOUT_PAGED5D:
+        if key_cache.stride()[2:] != (block_size * key_cache.shape[4], key_cache.shape[4], 1):
+            key_cache = key_cache.contiguous()
+        if value_cache.stride()[2:] != (block_size, 1):
+            value_cache = value_cache.contiguous()
     bt = _as_i32(block_tables)
     lens = _as_i32(context_lens)
     alibi = None if alibi_slopes is None else alibi_slopes.to(torch.float32).contiguous()
@@ -171,8 +201,8 @@ def _paged_attention(op, query, key_cache, value_cache, block_tables, context_le
             out.data_ptr(), query.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
             bt.data_ptr(), lens.data_ptr(), None if alibi is None else alibi.data_ptr(),
             B, Hq, num_kv_heads, D, block_size, bt.shape[1], max_seq_len, key_cache.shape[0],
-            float(scale), query.stride(0), key_cache.stride(0), key_cache.stride(1),
-            value_cache.stride(0), value_cache.stride(1), _lib.PKV_LAYOUT_PAGED5D, partition_size,
+            float(scale), query.stride(0), key_cache.stride(0), key_cache.stride(-2 if layout else 1),
+            value_cache.stride(0), value_cache.stride(-2 if layout else 1), layout, partition_size,
             ws.data_ptr(), ws.numel(), qc, cc, stream)
     _lib.check(st)
     return out

@@ -7,12 +7,12 @@ from .base_prefix_cache import (BasePrefixCache, EvictParams, EvictResult, Inser
 from .cache_init_params import CacheInitParams
 from .evict_policy import (EvictionStrategy, FIFOStrategy, FILOStrategy, LFUStrategy, LRUStrategy, MRUStrategy,
                            PriorityStrategy)
-from .memory_pool import MHATokenPool, PooledKVCache, TokenPoolAllocator
+from .memory_pool import MHATokenPool, PooledKVCache, TokenPoolAllocator, decode_batch
 from .paged_pool import BlockAllocator, BlockRadixCache, BlockTable, build_block_tables
 from .radix_cache import RadixCache, TreeNode
 
 __all__ = [
     "BasePrefixCache", "BlockAllocator", "BlockRadixCache", "BlockTable", "build_block_tables", "CacheInitParams", "EvictParams", "EvictResult", "EvictionStrategy", "FIFOStrategy",
     "FILOStrategy", "InsertParams", "InsertResult", "LFUStrategy", "LRUStrategy", "MHATokenPool", "MRUStrategy",
-    "MatchResult", "PooledKVCache", "PriorityStrategy", "RadixCache", "TokenPoolAllocator", "TreeNode",
+    "MatchResult", "PooledKVCache", "PriorityStrategy", "decode_batch", "RadixCache", "TokenPoolAllocator", "TreeNode",
 ]

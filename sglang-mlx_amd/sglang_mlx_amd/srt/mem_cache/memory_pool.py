@@ -13,6 +13,10 @@ per-request cache adapter (sglang_mlx/srt/mem_cache/memory_pool.py:27-269).
   [1, Hkv, T, D].
 * PooledKVCache -- the per-request, per-layer adapter with the mlx-lm cache
   protocol (set_indices / offset / update_and_fetch / state / make_mask).
+* Decode without the gather (the TODOs of memory_pool.py:110-115 and
+  :175-177): ``MHATokenPool.decode`` runs the paged decode kernel on the
+  pool's token rows with one slot table row per request (block size 1), and
+  ``decode_batch`` does so for a batch of PooledKVCache views.
 """
 
 from __future__ import annotations
@@ -104,6 +108,27 @@ class MHATokenPool:
         v = self.v_buffer[layer_idx].index_select(0, idx).transpose(0, 1).unsqueeze(0)
         return k, v
 
+    def decode(self, layer_idx: int, q: torch.Tensor, slot_lists, scale: float,
+               alibi_slopes: torch.Tensor | None = None) -> torch.Tensor:
+        """Decode attention of one query token per request over layer
+        ``layer_idx``: q [B, Hq, D]; slot_lists[i] lists request i's context
+        slots in order.  Returns [B, Hq, D] like q.  The kernel reads the
+        token rows in place (slot tables, block size 1); nothing is
+        gathered."""
+        B = q.shape[0]
+        if len(slot_lists) != B:
+            raise ValueError("one slot list per query row is required")
+        width = max((len(s) for s in slot_lists), default=0) or 1
+        table = np.full((B, width), -1, dtype=np.int32)
+        lens = np.zeros(B, dtype=np.int32)
+        for i, slots in enumerate(slot_lists):
+            table[i, :len(slots)] = np.asarray(list(slots), dtype=np.int32)
+            lens[i] = len(slots)
+        bt = torch.from_numpy(table).to(self.device, non_blocking=True)
+        ctx = torch.from_numpy(lens).to(self.device, non_blocking=True)
+        return _ext.paged_attention_v1(q, self.k_buffer[layer_idx], self.v_buffer[layer_idx], bt, ctx,
+                                       self.n_kv_heads, scale, 1, width, alibi_slopes)
+
 
 class PooledKVCache:
     """One request's view of one layer of the pool (mlx-lm cache protocol)."""
@@ -129,6 +154,11 @@ class PooledKVCache:
 
     def _live(self) -> list[int]:
         return self._prefix_indices + self._new_indices[:self._store_offset]
+
+    @property
+    def slot_indices(self) -> list[int]:
+        """Slots of every token of the request so far (prefix, then stored)."""
+        return self._live()
 
     def update_and_fetch(self, keys: torch.Tensor, values: torch.Tensor):
         """Store the next keys.shape[2] new tokens, then return every token of
@@ -165,3 +195,17 @@ class PooledKVCache:
         if window_size is not None:
             mask &= k > q - window_size
         return mask
+
+
+def decode_batch(caches: list[PooledKVCache], q: torch.Tensor, scale: float,
+                 alibi_slopes: torch.Tensor | None = None) -> torch.Tensor:
+    """Decode attention for a batch of requests that share one pool layer:
+    row i of q [B, Hq, D] attends over every token caches[i] holds (call it
+    after the step's update_and_fetch / store).  Continuous batching without
+    the per-request gather (memory_pool.py:175-177)."""
+    if not caches:
+        raise ValueError("decode_batch needs at least one cache")
+    pool, layer = caches[0]._pool, caches[0]._layer_idx
+    if any(c._pool is not pool or c._layer_idx != layer for c in caches):
+        raise ValueError("decode_batch caches must view the same pool layer")
+    return pool.decode(layer, q, [c.slot_indices for c in caches], scale, alibi_slopes)

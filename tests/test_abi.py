@@ -87,6 +87,29 @@ def test_paged_attention_rejects_misaligned_output():
     assert st == _lib.PKV_ERR_INVALID and "out must be 16-byte aligned" in err, (st, err)
 
 
+@pytest.mark.parametrize("kw,code,msg", [
+    # Rows narrower than Hkv heads of D, or heads closer than D apart.
+    (dict(kbs=16 * 255), 1, "rows that hold num_kv_heads heads"),
+    (dict(vhs=64), 1, "rows that hold num_kv_heads heads"),
+    (dict(kbs=16 * 256 + 1), 1, "rows that hold num_kv_heads heads"),
+    # Row ids are 32-bit.
+    (dict(nb=(1 << 31) // 16 + 1), 2, "at most 2^31 - 1 rows"),
+    (dict(bs=1, max_seq_len=4, kbs=256, vbs=256, nb=1 << 31), 2, "at most 2^31 - 1 rows"),
+    (dict(layout=2), 1, "Unknown cache layout"),
+])
+def test_token_row_rejections(kw, code, msg):
+    # Token-row layout [nb, 16, Hkv=2, D=128]: block stride 16 rows of 256.
+    import numpy as np
+    buf = np.zeros(64, dtype=np.uint8)
+    good = (buf.ctypes.data + 15) // 16 * 16
+    ptr = ctypes.c_void_p(good)
+    a = dict(out=ptr, q=ptr, kc=ptr, vc=ptr, bt=ptr, ctx=ptr, ws=ptr, ws_bytes=1 << 40,
+             layout=_lib.PKV_LAYOUT_TOKEN_MAJOR, kbs=16 * 256, khs=128, vbs=16 * 256, vhs=128)
+    a.update(kw)
+    st, err = attn(**a)
+    assert st == code and msg in err, (st, err)
+
+
 def test_paged_attention_empty_batch_is_a_noop():
     assert attn(B=0)[0] == _lib.PKV_OK
 

@@ -25,7 +25,8 @@ def pa_args(**kw):
 
 @pytest.mark.parametrize("kw,msg", [
     (dict(query=torch.zeros(2, 8, 64, 1, dtype=torch.float16)), "query must have shape"),
-    (dict(key_cache=torch.zeros(6, 2, 64, 16, dtype=torch.float16)), "must use paged attention layouts"),
+    (dict(value_cache=torch.zeros(6, 2, 64, dtype=torch.float16)), "must use paged attention layouts"),
+    (dict(key_cache=torch.zeros(6, 2, 64, 16, 8, 1, dtype=torch.float16)), "must use paged attention layouts"),
     (dict(block_tables=torch.zeros(8, dtype=torch.int32)), "block_tables must be 2D"),
     (dict(context_lens=torch.ones(3, dtype=torch.int32)), "sequence counts differ"),
     (dict(num_kv_heads=3), "num_heads must be divisible by num_kv_heads"),
@@ -44,6 +45,47 @@ def pa_args(**kw):
 def test_paged_attention_checks(kw, msg):
     with pytest.raises(ValueError, match=msg):
         kernels.paged_attention_v1(**pa_args(**kw))
+
+
+def rows_args(**kw):
+    # Token-row caches: MHATokenPool's [rows, Hkv, D] with a slot table (block size 1).
+    a = pa_args(key_cache=torch.zeros(96, 2, 64, dtype=torch.float16),
+                value_cache=torch.zeros(96, 2, 64, dtype=torch.float16), block_size=1,
+                block_tables=torch.zeros(2, 64, dtype=torch.int32))
+    a.update(kw)
+    return a
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(num_kv_heads=4), "cache KV-head count does not match"),
+    (dict(value_cache=torch.zeros(96, 2, 32, dtype=torch.float16)), "cache head size does not match"),
+    (dict(value_cache=torch.zeros(90, 2, 64, dtype=torch.float16)), "cache block dimensions do not match"),
+    (dict(block_size=16), "cache block dimensions do not match block_size"),
+    (dict(key_cache=torch.zeros(6, 16, 2, 64, dtype=torch.float16),
+          value_cache=torch.zeros(6, 16, 2, 64, dtype=torch.float16), block_size=8),
+     "cache block dimensions do not match block_size"),
+    (dict(key_cache=torch.zeros(6, 4, 2, 64, dtype=torch.float16),
+          value_cache=torch.zeros(6, 4, 2, 64, dtype=torch.float16), block_size=4),
+     "Unsupported head_size/block_size"),
+    (dict(key_cache=torch.zeros(96, 2, 64, dtype=torch.float16)[:, :, :32].repeat(1, 1, 2)[::1]), None),
+])
+def test_token_row_layout_checks(kw, msg):
+    if msg is None:
+        with pytest.raises(RuntimeError, match="GPU-only"):
+            kernels.paged_attention_v1(**rows_args(**kw))
+        return
+    with pytest.raises(ValueError, match=msg):
+        kernels.paged_attention_v1(**rows_args(**kw))
+
+
+def test_token_row_layout_rejects_strided_rows():
+    k = torch.zeros(96, 2, 128, dtype=torch.float16)[:, :, :64]
+    with pytest.raises(ValueError, match="rows must be contiguous"):
+        kernels.paged_attention_v1(**rows_args(key_cache=k))
+    # Flash layout whose blocks hold padding rows: block stride != block_size * row stride.
+    padded = torch.zeros(6, 10, 2, 64, dtype=torch.float16)[:, :8]
+    with pytest.raises(ValueError, match="rows must be contiguous"):
+        kernels.paged_attention_v1(**rows_args(key_cache=padded, value_cache=padded.clone(), block_size=8))
 
 
 def test_capacity_kat():
