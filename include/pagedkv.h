@@ -39,8 +39,11 @@ enum {
   PKV_ERR_HIP = 3
 };
 
-/* Element types (reference dtypeStr, mlx_paged_attention.cpp:30-37). */
-enum { PKV_F32 = 0, PKV_F16 = 1, PKV_BF16 = 2 };
+/* Element types (reference dtypeStr, mlx_paged_attention.cpp:30-37), and
+ * PKV_FP8_E4M3: one-byte E4M3 codes in the reference's format
+ * (float8.metal:13-124: bias 7, exponent 15 = +-inf / NaN, so finite values
+ * reach 240; not OCP E4M3FN), encoded by its algorithm bit for bit. */
+enum { PKV_F32 = 0, PKV_F16 = 1, PKV_BF16 = 2, PKV_FP8_E4M3 = 3 };
 
 /* KV cache layouts.
  *   PKV_LAYOUT_PAGED5D    : K [num_blocks, Hkv, D/x, block_size, x],
@@ -187,6 +190,25 @@ int pkv_copy_blocks(void* const* src_planes, void* const* dst_planes,
                     int32_t num_planes, int64_t src_blocks,
                     int64_t dst_blocks, int64_t block_bytes,
                     const int64_t* block_mapping, int64_t num_pairs,
+                    void* stream);
+
+/*
+ * Element-wise conversion with a scale.  Replaces convert_fp8_kernel
+ * (convert_fp8.metal:13-80, all 16 pairs of PKV_F32, PKV_F16, PKV_BF16 and
+ * PKV_FP8_E4M3), which the reference compiles but never binds:
+ *   FP8 -> T  : decode(code) * scale, rounded to T
+ *   T -> FP8  : encode(float(x) / scale)
+ *   FP8 -> FP8: encode(decode(code) * scale)
+ *   T -> U    : float(x) * scale, rounded to U
+ * Rounding to half / bfloat16 is to nearest even (bfloat16: NaN -> 0x7FC0).
+ * The encoder follows float8.metal:72-120 bit for bit, including its results
+ * for 256 <= |x| < 2^14 (small codes; 256 -> +0) and for values that round
+ * up to 2^-6 (+-0); from |x| >= 2^14, where the reference's shifts are
+ * undefined, it gives +-inf.  dst and src may be the same buffer when the
+ * element sizes are equal and must not otherwise overlap.
+ */
+int pkv_convert_fp8(void* dst, const void* src, int64_t num_elements,
+                    float scale, int32_t src_dtype, int32_t dst_dtype,
                     void* stream);
 
 /*

@@ -31,8 +31,21 @@ reference repository):
 - ``copy_blocks``, ``swap_blocks``
                            paged_attention/metal/cache/copy_blocks.metal:9-39, :55-70;
                            paged_attention/mlx_cache.cpp:302-370
+- ``fp8_e4m3_decode``      paged_attention/metal/float8.metal:13-38
+- ``fp8_e4m3_encode``      paged_attention/metal/float8.metal:72-124 (including
+                           its behaviour for 256 <= |x| < 2^14 and near 2^-6, kept
+                           as is; +-inf where its shifts are undefined)
+- ``convert_fp8``          paged_attention/metal/convert_fp8.metal:13-47
 
-Pinning (tests/test_oracle_*.py): bf16/fp16 rounding against torch's
+FP8 codes are ``uint8`` arrays (the reference's ``uchar``), format E4M3 with
+bias 7 in which exponent 15 is +-inf (mantissa 0) or NaN.
+
+Pinning (tests/test_oracle_*.py, tests/test_fp8_oracle.py): the FP8 decode
+table against torch's float8_e4m3fn on the 240 codes both formats share and
+known values elsewhere; the encoder by round trips over every finite code,
+torch's round-to-nearest-even in the normal range, brute-force nearest search
+in the subnormal range and explicit cases of its overflow and wrap-around
+behaviour; bf16/fp16 rounding against torch's
 conversions; the append against the element loop of the reference's own test
 and read-back invariants; attention against torch's float64
 scaled_dot_product_attention, closed forms (single token, equal keys,
@@ -350,3 +363,100 @@ def swap_blocks(src, dst, block_mapping):
         if 0 <= s < src.shape[0] and 0 <= d < out.shape[0]:
             out[d] = src[s]
     return out
+
+
+# ---------------------------------------------------------------------------
+# FP8 E4M3 (paged_attention/metal/float8.metal, convert_fp8.metal)
+# ---------------------------------------------------------------------------
+
+
+def fp8_e4m3_decode(codes: np.ndarray) -> np.ndarray:
+    """E4M3 codes -> float32 values (fp8_e4m3_to_float, float8.metal:13-38).
+
+    Bias 7; exponent 0 is zero or subnormal (mantissa/8 * 2^-6); exponent 15
+    is +-inf for mantissa 0 and NaN otherwise (not E4M3FN) -- the reference
+    returns an unsigned NAN there whatever the sign bit (:29-30); the rest is
+    (1 + mantissa/8) * 2^(exponent - 7).
+    """
+    c = np.asarray(codes, dtype=np.uint8).astype(np.int64)
+    s = c >> 7
+    e = (c >> 3) & 0xF
+    m = c & 7
+    mag = np.where(e == 0, m / 8.0 * 2.0 ** -6, (1.0 + m / 8.0) * np.exp2(np.minimum(e, 14) - 7.0))
+    val = np.where(s == 1, -mag, mag).astype(np.float32)
+    inf = np.where(s == 1, -np.inf, np.inf).astype(np.float32)
+    nan = np.full(c.shape, 0x7FC00000, dtype=np.uint32).view(np.float32)
+    return np.where(e == 15, np.where(m == 0, inf, nan), val).astype(np.float32)
+
+
+def fp8_e4m3_encode(x: np.ndarray) -> np.ndarray:
+    """float32 -> E4M3 codes, detail::fp32_to_fp8<4, 3, 7> (float8.metal:72-120).
+
+    Step by step as the reference:
+    * |x| inf or NaN: exponent 15, mantissa (NaN ? 1 : 0) (:80-83).
+    * Biased exponent e8 = e + 7 in [1, 14]: round the 23-bit mantissa to 3
+      bits to nearest even (:91-97); a carry moves to e8 + 1, and past 14 the
+      result is inf (:98-103).
+    * Otherwise (e8 < 1 -- and also e8 > 14, which the reference lets fall
+      through to this branch): e8 < -2 gives +-0 (:108-109); else the 24-bit
+      significand is shifted right by (1 - e8) + 20 with round-half-up and
+      only its low 3 bits are kept (:111-118).  So a value that rounds up to
+      2^-6 encodes as +-0, and 256 <= |x| < 2^14 lands on small codes
+      (256 -> +0).
+    * From |x| >= 2^14 (e8 >= 21) the reference's shift counts leave [0, 31]
+      (``1u << (rshift - 1)`` with rshift <= 0), which is undefined; this
+      restatement defines the result there as +-inf, the value of the
+      reference's own overflow branch.
+    """
+    u = np.asarray(x, dtype=np.float32).view(np.uint32).astype(np.int64)
+    s = (u >> 31) & 1
+    a = u & 0x7FFFFFFF
+    special = a >= 0x7F800000
+    e8 = ((a >> 23) & 0xFF) - 127 + 7
+    m = a & 0x7FFFFF
+    # normal path
+    shift = 20
+    mant = m >> shift
+    lsb = mant & 1
+    rnd = (m >> (shift - 1)) & 1
+    sticky = (m & ((1 << (shift - 1)) - 1)) != 0
+    mant = mant + (rnd & (sticky | lsb))
+    carry = (mant >> 3) != 0
+    e_n = np.where(carry, e8 + 1, e8)
+    mant_n = np.where(carry, 0, mant)
+    normal_code = np.where(e_n > 14, (s << 7) | (15 << 3), (s << 7) | (e_n << 3) | (mant_n & 7))
+    is_normal = (e8 >= 1) & (e8 <= 14)
+    # subnormal / underflow path (also reached for e8 > 14)
+    rshift = np.clip((1 - e8) + 20, 0, 63)
+    full = 0x800000 | m
+    rounded = (full + (np.int64(1) << np.maximum(rshift - 1, 0))) >> rshift
+    sub_code = np.where((e8 < -2) | (rounded == 0), s << 7, (s << 7) | (rounded & 7))
+    code = np.where(is_normal, normal_code, sub_code)
+    code = np.where(e8 >= 21, (s << 7) | (15 << 3), code)
+    code = np.where(special, (s << 7) | (15 << 3) | (a != 0x7F800000), code)
+    return code.astype(np.uint8)
+
+
+FP8 = "fp8_e4m3"
+
+
+def convert_fp8(src: np.ndarray, src_dtype: str, dst_dtype: str, scale: float) -> np.ndarray:
+    """convert_fp8_kernel<SRC_T, DST_T> (convert_fp8.metal:13-47), element-wise.
+
+    ``src``/result are storage arrays (uint8 codes for ``FP8``, uint16 bits for
+    float16/bfloat16, float32 values).  fp8 -> T: decode * scale (float32),
+    then rounded to T; T -> fp8: encode(float(x) / scale); fp8 -> fp8:
+    encode(decode * scale); T -> U: float(x) * scale rounded to U.  The
+    reference instantiates the 16 pairs of convert_fp8.metal:58-80.
+    """
+    sc = np.float32(scale)
+    if src_dtype == FP8:
+        v = fp8_e4m3_decode(src) * sc
+    else:
+        v = decode(src, src_dtype).astype(np.float32)
+        v = v / sc if dst_dtype == FP8 else v * sc
+    v = np.asarray(v, dtype=np.float32)
+    if dst_dtype == FP8:
+        return fp8_e4m3_encode(v)
+    return to_storage(v, dst_dtype)
+

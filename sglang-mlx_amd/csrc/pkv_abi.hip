@@ -321,6 +321,29 @@ int pkv_copy_blocks(void* const* src_planes, void* const* dst_planes, int32_t nu
   return PKV_OK;
 }
 
+int pkv_convert_fp8(void* dst, const void* src, int64_t num_elements, float scale, int32_t src_dtype,
+                    int32_t dst_dtype, void* stream) {
+  if (num_elements < 0) return fail(PKV_ERR_INVALID, "num_elements must be non-negative");
+  const bool types_ok = src_dtype >= PKV_F32 && src_dtype <= PKV_FP8_E4M3 && dst_dtype >= PKV_F32 &&
+                        dst_dtype <= PKV_FP8_E4M3;
+  if (!types_ok) return fail(PKV_ERR_UNSUPPORTED, "Unsupported dtype pair for convert_fp8");
+  if (num_elements == 0) return PKV_OK;
+  if (!dst || !src) return fail(PKV_ERR_INVALID, "null buffer");
+  const int sb = src_dtype == PKV_FP8_E4M3 ? 1 : elem_bytes(src_dtype);
+  const int db = dst_dtype == PKV_FP8_E4M3 ? 1 : elem_bytes(dst_dtype);
+  if ((reinterpret_cast<uintptr_t>(src) % sb) != 0 || (reinterpret_cast<uintptr_t>(dst) % db) != 0)
+    return fail(PKV_ERR_INVALID, "buffers are not aligned to their element size");
+  if (sb != db || src != dst) {
+    const uintptr_t s0 = reinterpret_cast<uintptr_t>(src), s1 = s0 + (uintptr_t)num_elements * sb;
+    const uintptr_t d0 = reinterpret_cast<uintptr_t>(dst), d1 = d0 + (uintptr_t)num_elements * db;
+    if (s0 < d1 && d0 < s1) return fail(PKV_ERR_INVALID, "dst and src overlap");
+  }
+  const hipError_t e = pkv::launch_convert_fp8(dst, src, num_elements, scale, src_dtype, dst_dtype,
+                                               static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "convert_fp8 launch");
+  return PKV_OK;
+}
+
 int pkv_get_device_attribute(int32_t attribute, int32_t device_id, int64_t* out) {
   if (!out) return fail(PKV_ERR_INVALID, "null output pointer");
   int v = 0;

@@ -14,6 +14,7 @@ namespace pkv {
 struct F32 {};
 struct F16 {};
 struct BF16 {};
+struct FP8 {};  // E4M3 codes in the reference's format (float8.metal:13-38)
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
@@ -33,6 +34,10 @@ template <> struct Elem<F16> {
 template <> struct Elem<BF16> {
   using storage = uint16_t;
   static constexpr int kBytes = 2;
+};
+template <> struct Elem<FP8> {
+  using storage = uint8_t;
+  static constexpr int kBytes = 1;
 };
 
 // ---- scalar conversions ---------------------------------------------------
@@ -54,6 +59,14 @@ __device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
 __device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
   return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
+// float -> fp16 of a value computed in float, rounded twice as written: the
+// empty asm keeps the compiler from fusing the producing multiply and this
+// conversion into v_fma_mixlo_f16 (a * b + 0), which rounds once and turns
+// -0 products into +0.
+__device__ __forceinline__ uint32_t f32_to_f16_bits_unfused(float f) {
+  asm volatile("" : "+v"(f));
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
 
 template <class T> __device__ __forceinline__ float to_f32(typename Elem<T>::storage v);
 template <> __device__ __forceinline__ float to_f32<F32>(float v) { return v; }
@@ -62,7 +75,9 @@ template <> __device__ __forceinline__ float to_f32<BF16>(uint16_t v) { return b
 
 template <class T> __device__ __forceinline__ typename Elem<T>::storage from_f32(float v);
 template <> __device__ __forceinline__ float from_f32<F32>(float v) { return v; }
-template <> __device__ __forceinline__ uint16_t from_f32<F16>(float v) { return (uint16_t)f32_to_f16_bits(v); }
+template <> __device__ __forceinline__ uint16_t from_f32<F16>(float v) {
+  return (uint16_t)f32_to_f16_bits_unfused(v);
+}
 template <> __device__ __forceinline__ uint16_t from_f32<BF16>(float v) { return (uint16_t)f32_to_bf16_bits(v); }
 
 // Element conversion used by the append: identical types copy bits, other

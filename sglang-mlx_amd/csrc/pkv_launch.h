@@ -9,7 +9,7 @@
 
 namespace pkv {
 
-enum { kF32 = 0, kF16 = 1, kBF16 = 2 };
+enum { kF32 = 0, kF16 = 1, kBF16 = 2, kFP8 = 3 };
 
 // Largest partition (tokens) of the partition kernel, for the internal v1
 // choice and for paged_attention_v2 callers alike; the tile height of the
@@ -45,6 +45,11 @@ struct RacParams {
 };
 
 hipError_t launch_reshape_and_cache(const RacParams& p, bool aligned, hipStream_t stream);
+
+// Element-wise conversion with a scale between the element types kF32,
+// kF16, kBF16 and kFP8 (E4M3 codes), convert_fp8.hip.
+hipError_t launch_convert_fp8(void* dst, const void* src, int64_t n, float scale, int src_dtype, int dst_dtype,
+                              hipStream_t stream);
 
 struct DecodeParams {
   void* out;                  // [B, Hq, D], query dtype

@@ -28,7 +28,9 @@ import torch
 from . import _lib
 
 _DTYPE_CODE = {torch.float32: _lib.PKV_F32, torch.float16: _lib.PKV_F16, torch.bfloat16: _lib.PKV_BF16}
-_ELEM_BYTES = {torch.float32: 4, torch.float16: 2, torch.bfloat16: 2}
+_ELEM_BYTES = {torch.float32: 4, torch.float16: 2, torch.bfloat16: 2, torch.uint8: 1}
+# uint8 tensors hold FP8 E4M3 codes (the reference's uchar, float8.metal).
+_FP8_DTYPE_CODE = {**_DTYPE_CODE, torch.uint8: _lib.PKV_FP8_E4M3}
 _HEAD_SIZES = (32, 64, 80, 96, 112, 120, 128, 192, 256)
 _BLOCK_SIZES = (8, 16, 32)
 
@@ -399,3 +401,30 @@ def get_max_shared_memory_per_block_device_attribute(device_id=0):
     v = ctypes.c_int64(0)
     _lib.check(_lib.lib().pkv_max_shared_memory_per_block(int(device_id), ctypes.byref(v)))
     return v.value
+
+
+def convert_fp8(dst, src, scale: float = 1.0):
+    """Element-wise conversion with a scale (convert_fp8.metal:13-80) between
+    float32, float16, bfloat16 and uint8 tensors of FP8 E4M3 codes: decode
+    then multiply into wider types, divide then encode into codes, multiply
+    between wider types.  Writes dst in place and returns it."""
+    _tensor(dst)
+    _tensor(src)
+    if dst.dtype not in _FP8_DTYPE_CODE or src.dtype not in _FP8_DTYPE_CODE:
+        raise ValueError(f"Unsupported dtype pair for convert_fp8: {src.dtype} -> {dst.dtype}")
+    if dst.numel() != src.numel():
+        raise ValueError("dst and src must have the same number of elements")
+    if not dst.is_contiguous():
+        raise ValueError("dst must be contiguous (it is written in place)")
+    dev = _on_gpu("ConvertFp8", dst, src)
+    if not src.is_contiguous():
+        src = src.contiguous()
+    n = src.numel()
+    if n == 0:
+        return dst
+    with torch.cuda.device(dev):
+        st = _lib.lib().pkv_convert_fp8(dst.data_ptr(), src.data_ptr(), n, float(scale),
+                                        _FP8_DTYPE_CODE[src.dtype], _FP8_DTYPE_CODE[dst.dtype], _stream(dev))
+    _lib.check(st)
+    return dst
+

@@ -19,7 +19,7 @@ PKV_ERR_INVALID = 1
 PKV_ERR_UNSUPPORTED = 2
 PKV_ERR_HIP = 3
 
-PKV_F32, PKV_F16, PKV_BF16 = 0, 1, 2
+PKV_F32, PKV_F16, PKV_BF16, PKV_FP8_E4M3 = 0, 1, 2, 3
 PKV_LAYOUT_PAGED5D, PKV_LAYOUT_TOKEN_MAJOR = 0, 1
 
 _c_void_p = ctypes.c_void_p
@@ -56,6 +56,9 @@ SIGNATURES = {
         ctypes.POINTER(_c_void_p), ctypes.POINTER(_c_void_p), _i32,  # src/dst planes, count
         _i64, _i64, _i64,                                            # src/dst blocks, block bytes
         _c_void_p, _i64, _c_void_p]),                                # mapping, pairs, stream
+    "pkv_convert_fp8": (ctypes.c_int, [
+        _c_void_p, _c_void_p, _i64, _f32,                            # dst, src, n, scale
+        _i32, _i32, _c_void_p]),                                     # src/dst dtype, stream
     "pkv_max_shared_memory_per_block": (ctypes.c_int, [_i32, ctypes.POINTER(_i64)]),
     "pkv_get_device_attribute": (ctypes.c_int, [_i32, _i32, ctypes.POINTER(_i64)]),
 }

@@ -8,6 +8,8 @@ Operations:
     reshape_and_cache    scatter new KV tokens into the cache (in place)
     copy_blocks          block copies inside the caches
     swap_blocks          block copies between two buffers
+    convert_fp8          element-wise conversion with a scale, FP8 E4M3 codes
+                         as uint8 tensors
 
 Tensors live on a HIP device; kernels run asynchronously on the current
 stream of that device.
@@ -103,3 +105,14 @@ def copy_blocks(
 def swap_blocks(src: torch.Tensor, dst: torch.Tensor, block_mapping: torch.Tensor) -> torch.Tensor:
     """Blit blocks between two buffers (metal_kernels.py:88-96)."""
     return _ext.swap_blocks(src, dst, block_mapping)
+
+
+def convert_fp8(dst: torch.Tensor, src: torch.Tensor, scale: float = 1.0) -> torch.Tensor:
+    """Element-wise precision conversion with a scale (the reference's
+    convert_fp8_kernel, convert_fp8.metal:13-80).  uint8 tensors hold FP8
+    E4M3 codes in the reference's format (bias 7, exponent 15 = inf / NaN).
+    fp8 -> T: decode * scale; T -> fp8: encode(x / scale); fp8 -> fp8:
+    encode(decode * scale); T -> U: x * scale.  dst is written in place and
+    returned."""
+    return _ext.convert_fp8(dst, src, scale)
+

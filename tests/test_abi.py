@@ -186,3 +186,26 @@ def test_status_translation():
         _lib.check(_lib.PKV_ERR_HIP)
     _lib.check(_lib.PKV_OK)
     assert lib.pkv_max_shared_memory_per_block(0, None) == _lib.PKV_ERR_INVALID
+
+
+def test_convert_fp8_rejections():
+    import numpy as np
+    lib = _lib.lib()
+    buf = np.zeros(256, dtype=np.uint8)
+    base = (buf.ctypes.data + 15) // 16 * 16
+    p = lambda off: ctypes.c_void_p(base + off)
+    cases = [
+        ((p(0), p(128), -1, 1.0, 0, 3), 1, "num_elements must be non-negative"),
+        ((p(0), p(128), 8, 1.0, 4, 3), 2, "Unsupported dtype pair"),
+        ((p(0), p(128), 8, 1.0, 0, -1), 2, "Unsupported dtype pair"),
+        ((None, p(128), 8, 1.0, 0, 3), 1, "null buffer"),
+        ((p(0), p(129), 8, 1.0, 0, 3), 1, "not aligned"),         # float32 source at an odd address
+        ((p(0), p(4), 8, 1.0, 0, 0), 1, "overlap"),
+        ((p(0), p(0), 8, 1.0, 0, 3), 1, "overlap"),               # in place needs equal element sizes
+    ]
+    for args, code, msg in cases:
+        st = lib.pkv_convert_fp8(*args, None)
+        err = lib.pkv_last_error().decode()
+        assert st == code and msg in err, (args, st, err)
+    assert lib.pkv_convert_fp8(p(0), p(128), 0, 1.0, 0, 3, None) == _lib.PKV_OK   # empty: no launch
+
