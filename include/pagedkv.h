@@ -80,7 +80,15 @@ const char* pkv_last_error(void);
  * num_slots   : num_blocks * block_size (PAGED5D) or the first dimension of
  *               the token-major buffers.
  * kv_dtype -> cache_dtype pairs: equal types, or F32 -> F16 / F32 -> BF16
- *               (round to nearest even; NaN -> 0x7FC0 for BF16).
+ *               (round to nearest even; NaN -> 0x7FC0 for BF16), or any of
+ *               F32 / F16 / BF16 -> PKV_FP8_E4M3.
+ * k_scale, v_scale: FP8 caches store encode(x / k_scale) for keys and
+ *               encode(x / v_scale) for values (the quantisation of
+ *               convert_fp8.metal:33-35; both finite and nonzero; a
+ *               power-of-two scale multiplies by its exact reciprocal, which
+ *               is the same result).  FP8 caches need 16-byte aligned
+ *               key/value rows and caches, and x = 16 in the paged layout.
+ *               Ignored for other caches (the reference has no FP8 append).
  */
 int pkv_reshape_and_cache(const void* key, const void* value,
                           void* key_cache, void* value_cache,
@@ -89,7 +97,8 @@ int pkv_reshape_and_cache(const void* key, const void* value,
                           int64_t key_stride, int64_t value_stride,
                           int32_t layout, int32_t block_size, int32_t x,
                           int64_t num_slots, int32_t kv_dtype,
-                          int32_t cache_dtype, void* stream);
+                          int32_t cache_dtype, float k_scale, float v_scale,
+                          void* stream);
 
 /*
  * Workspace bytes that pkv_paged_attention needs for these sizes

@@ -112,13 +112,17 @@ def decode(bits: np.ndarray, dtype: str) -> np.ndarray:
     raise ValueError(dtype)
 
 
-def convert_elements(src: np.ndarray, src_dtype: str, dst_dtype: str) -> np.ndarray:
+def convert_elements(src: np.ndarray, src_dtype: str, dst_dtype: str, scale: float = 1.0) -> np.ndarray:
     """static_cast<CACHE_T>(KV_T), reshape_and_cache.metal:9-12.
 
     Equal types copy the bits; float32 -> float16/bfloat16 rounds to nearest
     even.  The reference instantiates exactly these pairs
-    (reshape_and_cache.metal:91-95).
+    (reshape_and_cache.metal:91-95).  An FP8 cache (which the reference's
+    append does not have) stores encode(float(x) / scale), the quantisation
+    of convert_fp8.metal:33-35.
     """
+    if dst_dtype == FP8:
+        return fp8_e4m3_encode(decode(src, src_dtype).astype(np.float32) / np.float32(scale))
     if src_dtype == dst_dtype:
         return np.array(src, copy=True)
     if src_dtype != "float32":
@@ -132,7 +136,7 @@ def convert_elements(src: np.ndarray, src_dtype: str, dst_dtype: str) -> np.ndar
 
 
 def reshape_and_cache_paged5d(key, value, key_cache, value_cache, slot_mapping,
-                              kv_dtype: str, cache_dtype: str):
+                              kv_dtype: str, cache_dtype: str, k_scale: float = 1.0, v_scale: float = 1.0):
     """Scatter new tokens into the paged 5-D layout; returns new caches.
 
     key/value: [N, H, D] storage arrays.  key_cache [nb, H, D/x, bs, x],
@@ -152,8 +156,8 @@ def reshape_and_cache_paged5d(key, value, key_cache, value_cache, slot_mapping,
         return kc, vc
     s = slots[keep]
     blk, off = s // bs, s % bs
-    k = convert_elements(np.asarray(key)[tok], kv_dtype, cache_dtype)  # [n, H, D]
-    v = convert_elements(np.asarray(value)[tok], kv_dtype, cache_dtype)
+    k = convert_elements(np.asarray(key)[tok], kv_dtype, cache_dtype, k_scale)  # [n, H, D]
+    v = convert_elements(np.asarray(value)[tok], kv_dtype, cache_dtype, v_scale)
     # Two tokens naming one slot race on the GPU (the reference does not
     # order them either); the oracle lets the later token win.
     order = np.arange(tok.size)
@@ -169,7 +173,7 @@ def reshape_and_cache_paged5d(key, value, key_cache, value_cache, slot_mapping,
 
 
 def reshape_and_cache_token_major(key, value, key_cache, value_cache, slot_mapping,
-                                  kv_dtype: str, cache_dtype: str):
+                                  kv_dtype: str, cache_dtype: str, k_scale: float = 1.0, v_scale: float = 1.0):
     """Scatter into [num_slots, H, D] (MHATokenPool / flash layout).
 
     reshape_and_cache.metal:115-136 with slot = block*bs + offset, which is
@@ -186,8 +190,8 @@ def reshape_and_cache_token_major(key, value, key_cache, value_cache, slot_mappi
         s = slots[tok]
         _, last = np.unique(s[::-1], return_index=True)
         sel = np.arange(tok.size)[::-1][last]
-        kc[s[sel]] = convert_elements(np.asarray(key)[tok[sel]], kv_dtype, cache_dtype)
-        vc[s[sel]] = convert_elements(np.asarray(value)[tok[sel]], kv_dtype, cache_dtype)
+        kc[s[sel]] = convert_elements(np.asarray(key)[tok[sel]], kv_dtype, cache_dtype, k_scale)
+        vc[s[sel]] = convert_elements(np.asarray(value)[tok[sel]], kv_dtype, cache_dtype, v_scale)
     return kc.reshape(shape), vc.reshape(shape)
 
 

@@ -11,6 +11,7 @@
 #include "pkv_launch.h"
 
 #include <algorithm>
+#include <cmath>
 
 namespace {
 
@@ -25,7 +26,14 @@ int hip_fail(hipError_t e, const char* where) {
   return fail(PKV_ERR_HIP, std::string(where) + ": " + hipGetErrorString(e));
 }
 
-int elem_bytes(int32_t dt) { return dt == PKV_F32 ? 4 : 2; }
+int elem_bytes(int32_t dt) { return dt == PKV_F32 ? 4 : dt == PKV_FP8_E4M3 ? 1 : 2; }
+// Nonzero finite scale whose reciprocal is exact: a power of two whose
+// inverse is a normal float.
+bool exact_reciprocal(float s) {
+  int e = 0;
+  const float m = std::frexp(s, &e);
+  return std::isfinite(s) && (m == 0.5f || m == -0.5f) && e > -125 && e < 127;
+}
 bool valid_dtype(int32_t dt) { return dt == PKV_F32 || dt == PKV_F16 || dt == PKV_BF16; }
 bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
 
@@ -107,12 +115,16 @@ int pkv_reshape_and_cache(const void* key, const void* value, void* key_cache, v
                           const int32_t* slot_mapping, int64_t num_tokens, int32_t num_kv_heads,
                           int32_t head_size, int64_t key_stride, int64_t value_stride, int32_t layout,
                           int32_t block_size, int32_t x, int64_t num_slots, int32_t kv_dtype,
-                          int32_t cache_dtype, void* stream) {
+                          int32_t cache_dtype, float k_scale, float v_scale, void* stream) {
   if (num_tokens < 0) return fail(PKV_ERR_INVALID, "num_tokens must be non-negative");
   if (num_kv_heads <= 0 || head_size <= 0) return fail(PKV_ERR_INVALID, "num_kv_heads and head_size must be positive");
-  if (!valid_dtype(kv_dtype) || !valid_dtype(cache_dtype)) return fail(PKV_ERR_INVALID, "Unsupported dtype");
-  if (!(kv_dtype == cache_dtype || (kv_dtype == PKV_F32 && cache_dtype != PKV_F32)))
+  const bool fp8 = cache_dtype == PKV_FP8_E4M3;
+  if (!valid_dtype(kv_dtype) || !(valid_dtype(cache_dtype) || fp8))
+    return fail(PKV_ERR_INVALID, "Unsupported dtype");
+  if (!(kv_dtype == cache_dtype || fp8 || (kv_dtype == PKV_F32 && cache_dtype != PKV_F32)))
     return fail(PKV_ERR_UNSUPPORTED, "Unsupported key/cache dtype pair");
+  if (fp8 && !(std::isfinite(k_scale) && std::isfinite(v_scale) && k_scale != 0.f && v_scale != 0.f))
+    return fail(PKV_ERR_INVALID, "k_scale and v_scale must be finite and nonzero for FP8 caches");
   if (layout != PKV_LAYOUT_PAGED5D && layout != PKV_LAYOUT_TOKEN_MAJOR)
     return fail(PKV_ERR_INVALID, "Unknown cache layout");
   if (num_slots <= 0 || num_slots > INT32_MAX) return fail(PKV_ERR_INVALID, "num_slots must be in [1, 2^31)");
@@ -133,6 +145,8 @@ int pkv_reshape_and_cache(const void* key, const void* value, void* key_cache, v
   const bool aligned = aligned16(key) && aligned16(value) && aligned16(key_cache) && aligned16(value_cache) &&
                        (key_stride * kb) % 16 == 0 && (value_stride * kb) % 16 == 0 &&
                        (layout == PKV_LAYOUT_TOKEN_MAJOR || (head_size * kb) % 16 == 0);
+  if (fp8 && !aligned)
+    return fail(PKV_ERR_INVALID, "FP8 caches need 16-byte aligned key/value rows and caches");
   pkv::RacParams p;
   p.key = key;
   p.value = value;
@@ -149,6 +163,11 @@ int pkv_reshape_and_cache(const void* key, const void* value, void* key_cache, v
   p.layout = layout;
   p.kv_dtype = kv_dtype;
   p.cache_dtype = cache_dtype;
+  p.k_scale = k_scale;
+  p.v_scale = v_scale;
+  p.scales_pow2 = exact_reciprocal(k_scale) && exact_reciprocal(v_scale);
+  p.k_inv = p.scales_pow2 ? 1.f / k_scale : 0.f;
+  p.v_inv = p.scales_pow2 ? 1.f / v_scale : 0.f;
   const hipError_t e = pkv::launch_reshape_and_cache(p, aligned, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "reshape_and_cache launch");
   return PKV_OK;

@@ -42,6 +42,11 @@ struct RacParams {
   int32_t layout;  // 0 = paged 5-D, 1 = token-major
   int32_t kv_dtype;
   int32_t cache_dtype;
+  // FP8 caches store encode(x / scale); a power-of-two scale multiplies by
+  // its exact reciprocal instead (the same result, without a division).
+  float k_scale, v_scale;
+  float k_inv, v_inv;
+  int32_t scales_pow2;
 };
 
 hipError_t launch_reshape_and_cache(const RacParams& p, bool aligned, hipStream_t stream);

@@ -12,13 +12,14 @@
 //    (token, head): K leaves as D/x 16-byte chunks at a stride of bs*16 bytes,
 //    V as D single elements at a stride of bs elements (the layout makes V
 //    token-minor, so its stores cannot be wider than one element).
+//  * FP8 caches (E4M3 codes of x / scale, either layout): see below.
 //  * token-major (MHATokenPool / flash): K and V [num_slots, H, D].  A token's
 //    K row and V row are each one contiguous H*D run in both source and
 //    destination, so every lane moves 16-byte vectors and every wavefront
 //    covers 1 KiB of one row.  Rows of at least 64 vectors go one token per
 //    wavefront with nontemporal stores; shorter rows one token per
 //    workgroup.
-#include "pkv_device.h"
+#include "pkv_fp8.h"
 #include "pkv_launch.h"
 
 namespace pkv {
@@ -160,6 +161,105 @@ __global__ __launch_bounds__(256) void rac_token_major_wave_kernel(RacParams p) 
   }
 }
 
+// ---- FP8 caches -------------------------------------------------------------------
+// E4M3 codes of x / scale (pkv_fp8.h).  Token-major: one wavefront per
+// token, each lane turning 8 source elements into 8 code bytes per step of
+// the K row and of the V row.  Paged 5-D (x = 16): one wavefront per
+// (token, head), K as 16-byte chunks, V as single bytes (token-minor layout).
+__device__ __forceinline__ float fp8_scaled(float x, float scale, float inv, bool pow2) {
+  return pow2 ? x * inv : __fdiv_rn(x, scale);
+}
+
+template <class KT>
+__device__ __forceinline__ uint2 encode8(const typename Elem<KT>::storage* __restrict__ src, float scale, float inv,
+                                         bool pow2) {
+  float v[8];
+  if constexpr (std::is_same<KT, F32>::value) {
+    const float4 a = reinterpret_cast<const float4*>(src)[0], b = reinterpret_cast<const float4*>(src)[1];
+    v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+  } else {
+    const uint4 w = *reinterpret_cast<const uint4*>(src);
+    const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = to_f32<KT>((uint16_t)(u[i] & 0xffffu));
+      v[2 * i + 1] = to_f32<KT>((uint16_t)(u[i] >> 16));
+    }
+  }
+  uint32_t lo = 0, hi = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    lo |= fp8_e4m3_encode(fp8_scaled(v[i], scale, inv, pow2)) << (8 * i);
+    hi |= fp8_e4m3_encode(fp8_scaled(v[4 + i], scale, inv, pow2)) << (8 * i);
+  }
+  return make_uint2(lo, hi);
+}
+
+template <class KT>
+__global__ __launch_bounds__(256) void rac_fp8_token_major_kernel(RacParams p) {
+  using KS = typename Elem<KT>::storage;
+  const int lane = threadIdx.x & 63;
+  const int64_t tok = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tok >= p.num_tokens) return;
+  const int32_t slot = p.slot_mapping[tok];
+  if (slot < 0 || (int64_t)slot >= p.num_slots) return;
+  const int row = p.num_heads * p.head_size;  // a multiple of 8
+  const int n8 = row / 8;
+  const bool pow2 = p.scales_pow2 != 0;
+  const KS* ksrc = static_cast<const KS*>(p.key) + tok * p.key_stride;
+  const KS* vsrc = static_cast<const KS*>(p.value) + tok * p.value_stride;
+  uint8_t* kdst = static_cast<uint8_t*>(p.key_cache) + (int64_t)slot * row;
+  uint8_t* vdst = static_cast<uint8_t*>(p.value_cache) + (int64_t)slot * row;
+  for (int i = lane; i < n8; i += 64) {
+    const uint2 k = encode8<KT>(ksrc + 8 * i, p.k_scale, p.k_inv, pow2);
+    const uint2 v = encode8<KT>(vsrc + 8 * i, p.v_scale, p.v_inv, pow2);
+    __builtin_nontemporal_store(k.x, reinterpret_cast<uint32_t*>(kdst + 8 * i));
+    __builtin_nontemporal_store(k.y, reinterpret_cast<uint32_t*>(kdst + 8 * i) + 1);
+    __builtin_nontemporal_store(v.x, reinterpret_cast<uint32_t*>(vdst + 8 * i));
+    __builtin_nontemporal_store(v.y, reinterpret_cast<uint32_t*>(vdst + 8 * i) + 1);
+  }
+}
+
+template <class KT>
+__global__ __launch_bounds__(256) void rac_fp8_paged5d_kernel(RacParams p) {
+  using KS = typename Elem<KT>::storage;
+  const int lane = threadIdx.x & 63;
+  const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (wid >= p.num_tokens * p.num_heads) return;
+  const int64_t tok = wid / p.num_heads;
+  const int head = (int)(wid - tok * p.num_heads);
+  const int32_t slot = p.slot_mapping[tok];
+  if (slot < 0 || (int64_t)slot >= p.num_slots) return;
+  const int64_t blk = slot / p.block_size;
+  const int off = slot - (int)blk * p.block_size;
+  const int D = p.head_size;  // a multiple of 16
+  const bool pow2 = p.scales_pow2 != 0;
+  const KS* ksrc = static_cast<const KS*>(p.key) + tok * p.key_stride + (int64_t)head * D;
+  const KS* vsrc = static_cast<const KS*>(p.value) + tok * p.value_stride + (int64_t)head * D;
+  const int64_t region = ((int64_t)blk * p.num_heads + head) * (int64_t)D * p.block_size;
+  uint8_t* kdst = static_cast<uint8_t*>(p.key_cache) + region;    // [D/16][bs][16]
+  uint8_t* vdst = static_cast<uint8_t*>(p.value_cache) + region;  // [D][bs]
+  for (int c = lane; c < D / 8; c += 64) {  // 8-element halves of the 16-byte chunks
+    const uint2 k = encode8<KT>(ksrc + 8 * c, p.k_scale, p.k_inv, pow2);
+    *reinterpret_cast<uint2*>(kdst + ((int64_t)(c >> 1) * p.block_size + off) * 16 + (c & 1) * 8) = k;
+  }
+  for (int d = lane; d < D; d += 64)
+    vdst[(int64_t)d * p.block_size + off] =
+        (uint8_t)fp8_e4m3_encode(fp8_scaled(to_f32<KT>(vsrc[d]), p.v_scale, p.v_inv, pow2));
+}
+
+template <class KT>
+static hipError_t launch_rac_fp8(const RacParams& p, hipStream_t stream) {
+  if (p.layout == 0) {
+    const int64_t waves = p.num_tokens * p.num_heads;
+    hipLaunchKernelGGL((rac_fp8_paged5d_kernel<KT>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream, p);
+  } else {
+    hipLaunchKernelGGL((rac_fp8_token_major_kernel<KT>), dim3((unsigned)((p.num_tokens + 3) / 4)), dim3(256), 0,
+                       stream, p);
+  }
+  return hipGetLastError();
+}
+
 // ---- host launchers -----------------------------------------------------------------
 template <class KT, class CT>
 static hipError_t launch_rac_typed(const RacParams& p, bool aligned, hipStream_t stream) {
@@ -204,6 +304,12 @@ hipError_t launch_reshape_and_cache(const RacParams& p, bool aligned, hipStream_
   if (kt == kBF16 && ct == kBF16) return launch_rac_typed<BF16, BF16>(p, aligned, stream);
   if (kt == kF32 && ct == kF16) return launch_rac_typed<F32, F16>(p, aligned, stream);
   if (kt == kF32 && ct == kBF16) return launch_rac_typed<F32, BF16>(p, aligned, stream);
+  if (ct == kFP8) {
+    if (!aligned) return hipErrorInvalidValue;  // the ABI checks alignment first
+    if (kt == kF32) return launch_rac_fp8<F32>(p, stream);
+    if (kt == kF16) return launch_rac_fp8<F16>(p, stream);
+    if (kt == kBF16) return launch_rac_fp8<BF16>(p, stream);
+  }
   return hipErrorInvalidValue;
 }
 

@@ -21,6 +21,7 @@ Deliberate differences from the reference, all on inputs it cannot serve:
 
 from __future__ import annotations
 
+import math
 import threading
 
 import torch
@@ -233,7 +234,8 @@ def paged_attention_v2(query, key_cache, value_cache, block_tables, seq_lens, nu
                             num_kv_heads, scale, block_size, max_seq_len, alibi_slopes, partition_size)
 
 
-def _reshape_and_cache(op, key, value, key_cache, value_cache, slot_mapping, flash: bool):
+def _reshape_and_cache(op, key, value, key_cache, value_cache, slot_mapping, flash: bool,
+                       k_scale: float = 1.0, v_scale: float = 1.0):
     for t in (key, value, key_cache, value_cache, slot_mapping):
         _tensor(t)
     if key.dim() != 3 or value.shape != key.shape:
@@ -243,11 +245,19 @@ def _reshape_and_cache(op, key, value, key_cache, value_cache, slot_mapping, fla
     N, H, D = key.shape
     if value_cache.dtype != key_cache.dtype:
         raise ValueError("key_cache and value_cache dtypes differ")
-    kvc, cc = _dtype_code(key), _dtype_code(key_cache)
+    kvc = _dtype_code(key)
+    try:
+        cc = _FP8_DTYPE_CODE[key_cache.dtype]
+    except KeyError:
+        raise ValueError("Unsupported dtype") from None
     if value.dtype != key.dtype:
         raise ValueError("key and value dtypes differ")
-    if not (kvc == cc or kvc == _lib.PKV_F32):
+    fp8 = cc == _lib.PKV_FP8_E4M3
+    if not (kvc == cc or kvc == _lib.PKV_F32 or fp8):
         raise ValueError(f"Unsupported key/cache dtype pair: {key.dtype} -> {key_cache.dtype}")
+    k_scale, v_scale = float(k_scale), float(v_scale)
+    if fp8 and not all(math.isfinite(v) and v != 0.0 for v in (k_scale, v_scale)):
+        raise ValueError("k_scale and v_scale must be finite and nonzero for FP8 caches")
     x = 16 // _ELEM_BYTES[key_cache.dtype]
     if not flash and key_cache.dim() == 5:
         layout = _lib.PKV_LAYOUT_PAGED5D
@@ -285,24 +295,28 @@ def _reshape_and_cache(op, key, value, key_cache, value_cache, slot_mapping, fla
         st = lib.pkv_reshape_and_cache(
             key.data_ptr(), value.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
             slots.data_ptr(), N, H, D, key_stride, value_stride, layout, bs, x, num_slots,
-            kvc, cc, _stream(dev))
+            kvc, cc, k_scale, v_scale, _stream(dev))
     _lib.check(st)
     return [key_cache, value_cache]
 
 
-def reshape_and_cache(key, value, key_cache, value_cache, slot_mapping):
+def reshape_and_cache(key, value, key_cache, value_cache, slot_mapping, k_scale: float = 1.0,
+                      v_scale: float = 1.0):
     """Scatter new tokens into the cache in place; returns [key_cache, value_cache].
 
     Paged 5-D caches follow mlx_cache.cpp:256-278; 3-D [num_slots, Hkv, D]
-    caches (MHATokenPool buffers) use the token-major kernel.
+    caches (MHATokenPool buffers) use the token-major kernel.  uint8 caches
+    hold FP8 E4M3 codes of key / k_scale and value / v_scale (x = 16).
     """
-    return _reshape_and_cache("ReshapeAndCache", key, value, key_cache, value_cache, slot_mapping, False)
+    return _reshape_and_cache("ReshapeAndCache", key, value, key_cache, value_cache, slot_mapping, False,
+                              k_scale, v_scale)
 
 
-def reshape_and_cache_flash(key, value, key_cache, value_cache, slot_mapping):
+def reshape_and_cache_flash(key, value, key_cache, value_cache, slot_mapping, k_scale: float = 1.0,
+                            v_scale: float = 1.0):
     """Scatter into [num_blocks, block_size, Hkv, D] caches (mlx_cache.cpp:280-300)."""
     return _reshape_and_cache("ReshapeAndCacheFlash", key, value, key_cache, value_cache, slot_mapping,
-                              True)
+                              True, k_scale, v_scale)
 
 
 def _block_mapping(block_mapping) -> torch.Tensor:

@@ -38,6 +38,7 @@ SIGNATURES = {
         _i64, _i64,                                                # key/value stride
         _i32, _i32, _i32,                                          # layout, block_size, x
         _i64, _i32, _i32,                                          # num_slots, kv/cache dtype
+        _f32, _f32,                                                # k_scale, v_scale (FP8 caches)
         _c_void_p,                                                 # stream
     ]),
     "pkv_paged_attention_workspace_size": (_size, [_i32, _i32, _i32, _i32, _i32, _i32]),

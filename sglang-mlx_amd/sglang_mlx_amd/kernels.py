@@ -82,6 +82,8 @@ def reshape_and_cache(
     key_cache: torch.Tensor,
     value_cache: torch.Tensor,
     slot_mapping: torch.Tensor,
+    k_scale: float = 1.0,
+    v_scale: float = 1.0,
 ) -> list[torch.Tensor]:
     """Scatter-write new KV tokens into the cache (metal_kernels.py:64-74).
 
@@ -89,8 +91,10 @@ def reshape_and_cache(
     [num_tokens], -1 = padding (skipped).  The caches are updated in place
     and returned as [key_cache, value_cache].  Paged 5-D caches and 3-D
     MHATokenPool buffers [num_slots, num_kv_heads, head_size] are accepted.
+    uint8 caches hold FP8 E4M3 codes (the reference's format) of
+    key / k_scale and value / v_scale; the paged layout then has x = 16.
     """
-    return _ext.reshape_and_cache(key, value, key_cache, value_cache, slot_mapping)
+    return _ext.reshape_and_cache(key, value, key_cache, value_cache, slot_mapping, k_scale, v_scale)
 
 
 def copy_blocks(

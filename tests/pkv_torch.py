@@ -10,6 +10,8 @@ NAME_OF = {v: k for k, v in TORCH_DTYPE.items()}
 
 
 def to_torch(arr: np.ndarray, dtype: str, device="cuda") -> torch.Tensor:
+    if dtype == "fp8_e4m3":  # uint8 codes
+        return torch.from_numpy(np.ascontiguousarray(arr, dtype=np.uint8)).to(device)
     if dtype == "float32":
         t = torch.from_numpy(np.ascontiguousarray(arr, dtype=np.float32))
     else:
@@ -24,7 +26,7 @@ def to_index(arr: np.ndarray, device="cuda", dtype=torch.int32) -> torch.Tensor:
 def to_numpy(t: torch.Tensor) -> np.ndarray:
     """Storage array of a tensor (uint16 bits for 16-bit floats)."""
     t = t.detach().cpu().contiguous()
-    if t.dtype == torch.float32:
+    if t.dtype in (torch.float32, torch.uint8):
         return t.numpy()
     return t.view(torch.int16).numpy().view(np.uint16)
 

@@ -148,7 +148,7 @@ def test_workspace_size_closed_form():
 def rac(**kw):
     a = dict(key=None, value=None, kc=None, vc=None, slots=None, N=4, H=8, D=128, ks=1024, vs=1024,
              layout=_lib.PKV_LAYOUT_PAGED5D, bs=16, x=8, num_slots=1024, kvd=_lib.PKV_BF16, cd=_lib.PKV_BF16,
-             stream=None)
+             k_scale=1.0, v_scale=1.0, stream=None)
     a.update(kw)
     lib = _lib.lib()
     st = lib.pkv_reshape_and_cache(*a.values())
@@ -166,6 +166,12 @@ def rac(**kw):
     (dict(x=4), 1, "16 / sizeof(cache element)"),
     (dict(num_slots=1000), 1, "multiple of block_size"),
     (dict(), 1, "null buffer"),
+    (dict(kvd=_lib.PKV_FP8_E4M3, cd=_lib.PKV_FP8_E4M3, x=16), 1, "Unsupported dtype"),
+    (dict(cd=_lib.PKV_FP8_E4M3, x=8), 1, "16 / sizeof(cache element)"),
+    (dict(cd=_lib.PKV_FP8_E4M3, x=16, D=120), 1, "head_size must be a multiple of x"),
+    (dict(cd=_lib.PKV_FP8_E4M3, x=16, k_scale=0.0), 1, "finite and nonzero"),
+    (dict(cd=_lib.PKV_FP8_E4M3, x=16, v_scale=float("inf")), 1, "finite and nonzero"),
+    (dict(cd=_lib.PKV_FP8_E4M3, x=16), 1, "null buffer"),
 ])
 def test_reshape_and_cache_rejections(kw, code, msg):
     st, err = rac(**kw)
