@@ -158,7 +158,14 @@ size_t pkv_paged_attention_workspace_size(int32_t num_seqs, int32_t num_heads,
  *               PAGED5D).
  *               (The reference decodes the paged layout only; this is the
  *               gather-free path its pool asks for, memory_pool.py:110-112.)
- * (q_dtype, cache_dtype): (BF16,BF16), (F16,F16), (F32,BF16), (F32,F16).
+ * (q_dtype, cache_dtype): (BF16,BF16), (F16,F16), (F32,BF16), (F32,F16),
+ *   and (BF16|F16|F32, FP8_E4M3): FP8 caches in the paged layout (x = 16,
+ *   head_size a multiple of 16) hold codes of K / k_scale and V / v_scale
+ *   (pkv_reshape_and_cache); attention runs on decode(code) * scale, i.e.
+ *   scores scale * k_scale * (q . decode(k)) and output v_scale *
+ *   sum p decode(v) / (sum p + 1e-6).  The codes are dequantised exactly
+ *   into the query's 16-bit type (float16 for a float32 query).  k_scale and
+ *   v_scale are ignored for other caches.
  * head_size in {32,64,80,96,112,120,128,192,256}; block_size in {8,16,32}
  * (isValidConfig, mlx_paged_attention.cpp:52-59), or 1 with TOKEN_MAJOR.
  */
@@ -174,7 +181,8 @@ int pkv_paged_attention(void* out, const void* query, const void* key_cache,
                         int64_t v_block_stride, int64_t v_head_stride,
                         int32_t layout, int32_t partition_size,
                         void* workspace, size_t workspace_bytes,
-                        int32_t q_dtype, int32_t cache_dtype, void* stream);
+                        int32_t q_dtype, int32_t cache_dtype,
+                        float k_scale, float v_scale, void* stream);
 
 /*
  * Whole-block copies between paged caches.  A block is block_bytes

@@ -103,6 +103,8 @@ def to_storage(x: np.ndarray, dtype: str) -> np.ndarray:
 
 def decode(bits: np.ndarray, dtype: str) -> np.ndarray:
     """Storage representation -> float64 values."""
+    if dtype == FP8:
+        return fp8_e4m3_decode(bits).astype(np.float64)
     if dtype == "float32":
         return np.asarray(bits, dtype=np.float32).astype(np.float64)
     if dtype == "float16":
@@ -244,18 +246,24 @@ def alibi_bias(slopes: np.ndarray, ctx: int) -> np.ndarray:
 
 def paged_attention(q, key_cache, value_cache, block_tables, context_lens, num_kv_heads: int,
                     scale: float, block_size: int, max_seq_len: int, alibi_slopes=None,
-                    q_dtype: str = "float32", cache_dtype: str = "float32") -> np.ndarray:
+                    q_dtype: str = "float32", cache_dtype: str = "float32",
+                    k_scale: float = 1.0, v_scale: float = 1.0) -> np.ndarray:
     """paged_attention_v1 in float64 -> [B, Hq, D] float64.
 
     Follows paged_attention_kernels.metal:37-168: zero output when
     ctx == 0 or ctx > max_seq_len (:44-50, context read as uint32),
     GQA map h // (Hq/Hkv) (:57-58), fp32-exact inputs, denominator
     sum + 1e-6 (:144).  ``block_size`` is implied by the cache shape and
-    only cross-checked.
+    only cross-checked.  FP8 caches (an extension; the reference's decode
+    reads 16/32-bit caches only) are read as decode(code) * k_scale and
+    decode(code) * v_scale, the dequantisation of convert_fp8.metal:27-29.
     """
     q64 = decode(q, q_dtype)
     kc64 = decode(key_cache, cache_dtype)
     vc64 = decode(value_cache, cache_dtype)
+    if cache_dtype == FP8:
+        kc64 = kc64 * k_scale
+        vc64 = vc64 * v_scale
     assert kc64.shape[3] == block_size
     B, Hq, D = q64.shape
     assert Hq % num_kv_heads == 0

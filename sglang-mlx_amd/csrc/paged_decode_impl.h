@@ -40,7 +40,7 @@
 // reference's single softmax.
 #pragma once
 
-#include "pkv_device.h"
+#include "pkv_fp8.h"
 #include "pkv_launch.h"
 
 namespace pkv {
@@ -98,14 +98,29 @@ template <> __device__ __forceinline__ void split_q<F16>(float x, uint32_t& hi, 
   lo = f32_to_f16_bits(x - f16_bits_to_f32(hi));
 }
 
-// One wavefront's 16-token tile in registers.
-template <int D> struct Tile {
+// MFMA operand type of a (query, cache) type pair: the cache type, or for
+// FP8 caches the query's 16-bit type (E4M3 values are exact in both) and
+// float16 for a float32 query (more mantissa for its hi/lo split).
+template <class QT, class CT> struct MmaOf { using type = CT; };
+template <class QT> struct MmaOf<QT, FP8> {
+  using type = std::conditional_t<std::is_same<QT, BF16>::value, BF16, F16>;
+};
+
+// One wavefront's 16-token tile in registers, as MFMA operands.
+template <int D, bool F8 = false> struct Tile {
   static constexpr int KSTEPS = (D + 31) / 32;  // 16x16x32 k-steps over the head dimension
   static constexpr int DT = (D + 15) / 16;      // 16-wide dimension tiles of the output
   uint4 k[KSTEPS];
   uint2 v[DT];
   int kpb;  // block of this lane's K row (token tt0 + col), -1 if masked out
   int vpb;  // block of this lane's 4 V tokens, -1 if masked out
+};
+// FP8 caches: the tile arrives as raw codes (8 K codes per k-step, 4 V codes
+// per dimension tile: half the bytes of a 16-bit tile, the same number of
+// loads) and is dequantised into k / v when consumed.
+template <int D> struct Tile<D, true> : Tile<D, false> {
+  uint2 k8[Tile<D, false>::KSTEPS];
+  uint32_t v8[Tile<D, false>::DT];
 };
 
 // Register sets per wavefront (tiles in flight + 1), as many as leave room
@@ -193,6 +208,92 @@ __device__ __forceinline__ void load_tile(Tile<D>& t, const uint16_t* kbase, con
       else
         t.v[dt] = make_uint2(0, 0);
     }
+  }
+}
+
+// load_tile for FP8 caches in the paged 5-D layout with x = 16: K [D/16][bs][16]
+// bytes, V [D][bs] bytes per (block, head).  Lane (g, col) takes the 8 codes
+// of k-step j that the 16-bit path gives it (dimensions 8(4j + g) .. +7, the
+// half g & 1 of 16-byte chunk 2j + g/2 of token col), and the 4 V codes of
+// tokens 4g .. 4g+3 of dimension 16dt + col.  Same addressing schemes as
+// load_tile: buffer resources with a wave-uniform token offset for blocks of
+// 16 and more, per-lane addresses (masked blocks read block 0) for 8.
+template <int D, int BS>
+__device__ __forceinline__ void load_tile_fp8(Tile<D, true>& t, const uint8_t* kbase, const uint8_t* vbase,
+                                              int64_t k_block_stride, int64_t v_block_stride, int b0, int b1, int tt0,
+                                              int g, int col) {
+  constexpr int NCHUNK = D / 8;  // 8-code K groups per token
+  if constexpr (BS >= kTile) {
+    const int b = b0;
+    t.kpb = t.vpb = b;
+    const int off = tt0 % BS;
+    const int64_t bb = b < 0 ? 0 : b;
+    const int bytes = b < 0 ? 0 : D * BS;
+    const __amdgpu_buffer_rsrc_t kr =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(kbase + bb * k_block_stride), (short)0, bytes, kBufferRsrcWord3);
+    const __amdgpu_buffer_rsrc_t vr =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(vbase + bb * v_block_stride), (short)0, bytes, kBufferRsrcWord3);
+    const int ko = (g >> 1) * (BS * 16) + col * 16 + (g & 1) * 8;
+    const int vo = col * BS + 4 * g;
+#pragma unroll
+    for (int j = 0; j < Tile<D>::KSTEPS; ++j) {
+      const int c = 4 * j + g;
+      t.k8[j] = (NCHUNK % 4 == 0 || c < NCHUNK)
+                    ? __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(kr, ko + j * (2 * BS * 16),
+                                                                                      off * 16, 0))
+                    : make_uint2(0, 0);
+    }
+#pragma unroll
+    for (int dt = 0; dt < Tile<D>::DT; ++dt)
+      t.v8[dt] = __builtin_amdgcn_raw_buffer_load_b32(vr, vo + dt * (16 * BS), off, 0);
+  } else {
+    const int kpb = col < 8 ? b0 : b1;  // K row = token tt0 + col
+    t.kpb = kpb;
+    const uint8_t* kp = kbase + (int64_t)(kpb < 0 ? 0 : kpb) * k_block_stride + (col % BS) * 16 + (g & 1) * 8 +
+                        (g >> 1) * (BS * 16);
+    const int vpb = g < 2 ? b0 : b1;  // V tokens tt0 + 4g .. +3
+    t.vpb = vpb;
+    const uint8_t* vp = vbase + (int64_t)(vpb < 0 ? 0 : vpb) * v_block_stride + ((4 * g) % BS) + col * BS;
+#pragma unroll
+    for (int j = 0; j < Tile<D>::KSTEPS; ++j) {
+      const int c = 4 * j + g;
+      t.k8[j] = (NCHUNK % 4 == 0 || c < NCHUNK) ? *reinterpret_cast<const uint2*>(kp + j * (2 * BS * 16))
+                                                : make_uint2(0, 0);
+    }
+#pragma unroll
+    for (int dt = 0; dt < Tile<D>::DT; ++dt) t.v8[dt] = *reinterpret_cast<const uint32_t*>(vp + dt * (16 * BS));
+  }
+}
+
+// Raw FP8 codes -> MFMA operands (MT = BF16 or F16), exactly: the hardware
+// conversion, and for the rare tile holding a code with exponent 15 (which
+// the hardware reads as an E4M3FN number) the reference's inf / NaN.
+template <class MT, int D> __device__ __forceinline__ void dequant_tile(Tile<D, true>& t) {
+  constexpr int KSTEPS = Tile<D>::KSTEPS;
+  constexpr int DT = Tile<D>::DT;
+  uint32_t probe = 0;
+#pragma unroll
+  for (int j = 0; j < KSTEPS; ++j) {
+    probe |= (t.k8[j].x & 0x78787878u) + 0x08080808u;
+    probe |= (t.k8[j].y & 0x78787878u) + 0x08080808u;
+  }
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) probe |= (t.v8[dt] & 0x78787878u) + 0x08080808u;
+#pragma unroll
+  for (int j = 0; j < KSTEPS; ++j) {
+    const uint2 lo = fp8x4_cvt<MT>(t.k8[j].x), hi = fp8x4_cvt<MT>(t.k8[j].y);
+    t.k[j] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+  }
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) t.v[dt] = fp8x4_cvt<MT>(t.v8[dt]);
+  if (__any((probe & 0x80808080u) != 0u)) {
+#pragma unroll
+    for (int j = 0; j < KSTEPS; ++j) {
+      const uint2 lo = fp8x4_exact<MT>(t.k8[j].x), hi = fp8x4_exact<MT>(t.k8[j].y);
+      t.k[j] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) t.v[dt] = fp8x4_exact<MT>(t.v8[dt]);
   }
 }
 
@@ -517,7 +618,8 @@ __device__ __forceinline__ void load_query(const DecodeParams& p, int seq, int h
 // tiles each keep the memory system just as busy).
 template <class QT, class CT, int D, int BS, int NW, int MAXT, int MAXBUF = 4, bool ROWS = false,
           class Blocks = WaveBlocks<BS, MAXT>>
-__device__ __forceinline__ void stream_tiles(const DecodeParams& p, const uint16_t* kbase, const uint16_t* vbase,
+__device__ __forceinline__ void stream_tiles(const DecodeParams& p, const typename Elem<CT>::storage* kbase,
+                                             const typename Elem<CT>::storage* vbase,
                                              const Blocks& blk, int t0, int t1, uint32_t ctx,
                                              int first, int g, int col, const uint4 (&qa)[Tile<D>::KSTEPS],
                                              const uint4 (&qb)[std::is_same<QT, F32>::value ? Tile<D>::KSTEPS : 1],
@@ -526,6 +628,9 @@ __device__ __forceinline__ void stream_tiles(const DecodeParams& p, const uint16
   constexpr int DT = Tile<D>::DT;
   constexpr bool SPLIT_Q = std::is_same<QT, F32>::value;
   constexpr int PT = WaveBlocks<BS, MAXT>::PER_TILE;
+  constexpr bool F8 = std::is_same<CT, FP8>::value;
+  using MT = typename MmaOf<QT, CT>::type;
+  using TileT = Tile<D, F8>;
   const int ntiles = (t1 - t0 + kTile - 1) / kTile;
   const int nfull = (t1 - t0) / kTile;  // tiles entirely inside [t0, t1)
   if (first >= ntiles) return;
@@ -548,9 +653,10 @@ __device__ __forceinline__ void stream_tiles(const DecodeParams& p, const uint16
   // contribute nothing either.  Masked tokens get score -inf and V zero (a
   // slot may hold anything, including NaN); with block_size >= 16 a masked
   // block's loads already returned zero, so only its scores need masking.
-  auto consume = [&](auto tail_tag, Tile<D>& t, int tt0) {
+  auto consume = [&](auto tail_tag, TileT& t, int tt0) {
     constexpr bool TAIL = decltype(tail_tag)::value;
     const int vtok = tt0 + 4 * g;
+    if constexpr (F8) dequant_tile<MT, D>(t);
     if constexpr (ROWS) transpose_tile_rows<D>(t, col);
     bool zero_v = false;
     if constexpr (TAIL) {
@@ -584,8 +690,8 @@ __device__ __forceinline__ void stream_tiles(const DecodeParams& p, const uint16
     f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < KSTEPS; ++j) {
-      sacc = Mma<CT>::k32(t.k[j], qa[j], sacc);
-      if constexpr (SPLIT_Q) sacc = Mma<CT>::k32(t.k[j], qb[j], sacc);
+      sacc = Mma<MT>::k32(t.k[j], qa[j], sacc);
+      if constexpr (SPLIT_Q) sacc = Mma<MT>::k32(t.k[j], qb[j], sacc);
     }
     // ---- online softmax (log2 domain) ----
     float sc[4];
@@ -625,20 +731,24 @@ __device__ __forceinline__ void stream_tiles(const DecodeParams& p, const uint16
     for (int r = 0; r < 4; ++r) pr[r] = fast_exp2(sc[r] - m_use);
     acc.l_run += (pr[0] + pr[1]) + (pr[2] + pr[3]);
     // ---- O^T += V^T * P^T ----
-    const uint2 pp = make_uint2(pack_p<CT>(pr[0], pr[1]), pack_p<CT>(pr[2], pr[3]));
+    const uint2 pp = make_uint2(pack_p<MT>(pr[0], pr[1]), pack_p<MT>(pr[2], pr[3]));
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) acc.o[dt] = Mma<CT>::k16(t.v[dt], pp, acc.o[dt]);
+    for (int dt = 0; dt < DT; ++dt) acc.o[dt] = Mma<MT>::k16(t.v[dt], pp, acc.o[dt]);
   };
   using Full = std::integral_constant<bool, false>;
   using Tail = std::integral_constant<bool, true>;
-  auto load = [&](Tile<D>& t, int tile) {
+  auto load = [&](TileT& t, int tile) {
     if constexpr (ROWS) {
       blk.template load_tile<D>(t, p, kbase, vbase, tile, (tile - first) / NW, g, col);
     } else {
       const int k = (tile - first) / NW;
       const int b0 = blk.get(k * PT);
       const int b1 = PT == 2 ? blk.get(k * PT + 1) : b0;
-      load_tile<D, BS>(t, kbase, vbase, p.k_block_stride, p.v_block_stride, b0, b1, t0 + tile * kTile, g, col);
+      if constexpr (F8)
+        load_tile_fp8<D, BS>(t, kbase, vbase, p.k_block_stride, p.v_block_stride, b0, b1, t0 + tile * kTile, g,
+                             col);
+      else
+        load_tile<D, BS>(t, kbase, vbase, p.k_block_stride, p.v_block_stride, b0, b1, t0 + tile * kTile, g, col);
     }
   };
 
@@ -651,7 +761,7 @@ __device__ __forceinline__ void stream_tiles(const DecodeParams& p, const uint16
   // rotating tile sets tight.)
   if (first < nfull) {
     const int last = first + ((nfull - 1 - first) / NW) * NW;
-    Tile<D> t[NBUF];
+    TileT t[NBUF];
 #pragma unroll
     for (int b = 0; b < NBUF - 1; ++b) load(t[b], min(first + b * NW, last));
     int tile = first;
@@ -669,7 +779,7 @@ __device__ __forceinline__ void stream_tiles(const DecodeParams& p, const uint16
   }
   // The tile that crosses t1, if this wavefront owns it.
   if (nfull < ntiles && nfull >= first && (nfull - first) % NW == 0) {
-    Tile<D> tt;
+    TileT tt;
     load(tt, nfull);
     consume(Tail{}, tt, t0 + nfull * kTile);
   }
@@ -730,7 +840,7 @@ template <class QT, int D, bool ROWS = false>
 __device__ __forceinline__ void write_output(const DecodeParams& p, int64_t hrow, const WaveAcc<D>& acc, float L,
                                              int g) {
   using QS = typename Elem<QT>::storage;
-  const float inv = 1.f / (L + 1e-6f);
+  const float inv = p.v_scale / (L + 1e-6f);
   QS* out = static_cast<QS*>(p.out) + hrow * D;
 #pragma unroll
   for (int dt = 0; dt < Tile<D>::DT; ++dt)
@@ -797,7 +907,7 @@ __device__ __forceinline__ void merge_store_waves(const DecodeParams& p, WaveAcc
     aw[w] = exp2f(s_m[w][col] - mu);
     L += s_l[w][col] * aw[w];
   }
-  const float inv = 1.f / (L + 1e-6f);
+  const float inv = p.v_scale / (L + 1e-6f);
   QS* out = static_cast<QS*>(p.out) + (hrow0 + col) * D;
   for (int dt = wave; dt < DT; dt += NW) {
     const int d0 = tile_dim<D, ROWS>(dt, g);
@@ -874,13 +984,14 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_part_kernel(DecodeParams
   blk.load(p.block_tables + (int64_t)seq * p.max_blocks_per_seq, p.num_blocks, nlb, lb0, t0, wave, NW, lane);
   uint4 qa[KSTEPS];
   uint4 qb[SPLIT_Q ? KSTEPS : 1];
-  load_query<QT, CT, D>(p, seq, h0, nh, g, col, qa, qb);
+  load_query<QT, typename MmaOf<QT, CT>::type, D>(p, seq, h0, nh, g, col, qa, qb);
   const float slope = (p.alibi != nullptr && col < nh) ? p.alibi[h0 + col] * kLog2e : 0.f;
 
   WaveAcc<D> acc;
   acc.init();
-  const uint16_t* kbase = static_cast<const uint16_t*>(p.k_cache) + (int64_t)kvh * p.k_head_stride;
-  const uint16_t* vbase = static_cast<const uint16_t*>(p.v_cache) + (int64_t)kvh * p.v_head_stride;
+  using CS = typename Elem<CT>::storage;
+  const CS* kbase = static_cast<const CS*>(p.k_cache) + (int64_t)kvh * p.k_head_stride;
+  const CS* vbase = static_cast<const CS*>(p.v_cache) + (int64_t)kvh * p.v_head_stride;
   // Two tile buffers: fewer registers, more resident workgroups per CU
   // (measured 1-4% faster than three or four at 32K-128K contexts).
   stream_tiles<QT, CT, D, BS, NW, MAXT, 2>(p, kbase, vbase, blk, t0, t1, ctx, wave, g, col, qa, qb, slope, acc);
@@ -894,7 +1005,7 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_part_kernel(DecodeParams
     return;
   }
   const int64_t slot = hrow * p.max_parts + part;
-  const float invl = L > 0.f ? 1.f / L : 0.f;
+  const float invl = L > 0.f ? p.v_scale / L : 0.f;
   float* wo = p.ws_o + slot * D;
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) {
@@ -966,13 +1077,14 @@ __global__ __launch_bounds__(64 * kPartWaves) void paged_decode_rows_kernel(Deco
 
   uint4 qa[KSTEPS];
   uint4 qb[SPLIT_Q ? KSTEPS : 1];
-  load_query<QT, CT, D>(p, seq, h0, nh, g, col, qa, qb);
+  load_query<QT, typename MmaOf<QT, CT>::type, D>(p, seq, h0, nh, g, col, qa, qb);
   const float slope = (p.alibi != nullptr && col < nh) ? p.alibi[h0 + col] * kLog2e : 0.f;
 
   WaveAcc<D> acc;
   acc.init();
-  const uint16_t* kbase = static_cast<const uint16_t*>(p.k_cache) + (int64_t)kvh * p.k_head_stride;
-  const uint16_t* vbase = static_cast<const uint16_t*>(p.v_cache) + (int64_t)kvh * p.v_head_stride;
+  using CS = typename Elem<CT>::storage;
+  const CS* kbase = static_cast<const CS*>(p.k_cache) + (int64_t)kvh * p.k_head_stride;
+  const CS* vbase = static_cast<const CS*>(p.v_cache) + (int64_t)kvh * p.v_head_stride;
   stream_tiles<QT, CT, D, kTile, NW, 1, 2, true, LdsRows>(p, kbase, vbase, LdsRows{s_rows}, t0, t1, ctx, wave, g, col,
                                                          qa, qb, slope, acc);
 
@@ -985,7 +1097,7 @@ __global__ __launch_bounds__(64 * kPartWaves) void paged_decode_rows_kernel(Deco
     return;
   }
   const int64_t slot = hrow * p.max_parts + part;
-  const float invl = L > 0.f ? 1.f / L : 0.f;
+  const float invl = L > 0.f ? p.v_scale / L : 0.f;
   float* wo = p.ws_o + slot * D;
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) {
@@ -1106,7 +1218,7 @@ __global__ __launch_bounds__(64 * (Persist<D, BS == 0>::kWaves)) void paged_deco
   load_blocks(it.seq, blk);
   uint4 qa[KSTEPS];
   uint4 qb[SPLIT_Q ? KSTEPS : 1];
-  load_query<QT, CT, D>(p, it.seq, it.h0, it.nh, g, col, qa, qb);
+  load_query<QT, typename MmaOf<QT, CT>::type, D>(p, it.seq, it.h0, it.nh, g, col, qa, qb);
   float slope = (p.alibi != nullptr && col < it.nh) ? p.alibi[it.h0 + col] * kLog2e : 0.f;
 
   int buf = 0;
@@ -1122,15 +1234,16 @@ __global__ __launch_bounds__(64 * (Persist<D, BS == 0>::kWaves)) void paged_deco
     if (has_next) {
       nit = item_at(nrank);
       load_blocks(nit.seq, nblk);
-      load_query<QT, CT, D>(p, nit.seq, nit.h0, nit.nh, g, col, nqa, nqb);
+      load_query<QT, typename MmaOf<QT, CT>::type, D>(p, nit.seq, nit.h0, nit.nh, g, col, nqa, nqb);
       nslope = (p.alibi != nullptr && col < nit.nh) ? p.alibi[nit.h0 + col] * kLog2e : 0.f;
     }
 
     WaveAcc<D> acc;
     acc.init();
     if (it.live) {
-      const uint16_t* kbase = static_cast<const uint16_t*>(p.k_cache) + (int64_t)it.kvh * p.k_head_stride;
-      const uint16_t* vbase = static_cast<const uint16_t*>(p.v_cache) + (int64_t)it.kvh * p.v_head_stride;
+      using CS = typename Elem<CT>::storage;
+      const CS* kbase = static_cast<const CS*>(p.k_cache) + (int64_t)it.kvh * p.k_head_stride;
+      const CS* vbase = static_cast<const CS*>(p.v_cache) + (int64_t)it.kvh * p.v_head_stride;
       if constexpr (ROWS) {
         // Every head's rows end within k_rows_bytes (v_rows_bytes) of its base.
         blk.kr = __builtin_amdgcn_make_buffer_rsrc((void*)kbase, (short)0, (int)p.k_rows_bytes, kBufferRsrcWord3);
@@ -1335,10 +1448,24 @@ static hipError_t launch_rows(const DecodeParams& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// FP8 caches: paged 5-D layout only, head sizes that are multiples of x = 16.
 template <class QT, class CT, int D>
 static hipError_t launch_layout(const DecodeParams& p, int block_size, hipStream_t stream, bool* ok) {
-  if (p.rows) return launch_rows<QT, CT, D>(p, stream);
-  return launch_bs<QT, CT, D>(p, block_size, stream, ok);
+  if constexpr (std::is_same<CT, FP8>::value) {
+    if constexpr (D % 16 != 0) {
+      *ok = false;
+      return hipErrorInvalidValue;
+    } else {
+      if (p.rows) {
+        *ok = false;
+        return hipErrorInvalidValue;
+      }
+      return launch_bs<QT, CT, D>(p, block_size, stream, ok);
+    }
+  } else {
+    if (p.rows) return launch_rows<QT, CT, D>(p, stream);
+    return launch_bs<QT, CT, D>(p, block_size, stream, ok);
+  }
 }
 
 template <class QT, class CT>

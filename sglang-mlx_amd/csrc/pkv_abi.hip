@@ -189,7 +189,7 @@ int pkv_paged_attention(void* out, const void* query, const void* key_cache, con
                         int64_t num_blocks, float scale, int64_t q_stride, int64_t k_block_stride,
                         int64_t k_head_stride, int64_t v_block_stride, int64_t v_head_stride, int32_t layout,
                         int32_t partition_size, void* workspace, size_t workspace_bytes, int32_t q_dtype,
-                        int32_t cache_dtype, void* stream) {
+                        int32_t cache_dtype, float k_scale, float v_scale, void* stream) {
   if (num_seqs < 0) return fail(PKV_ERR_INVALID, "num_seqs must be non-negative");
   int32_t ps = 0, parts = 0;
   const int st = resolve_partition(num_seqs, num_heads, num_kv_heads, max_seq_len, block_size, partition_size,
@@ -202,10 +202,16 @@ int pkv_paged_attention(void* out, const void* query, const void* key_cache, con
   const bool rows = layout == PKV_LAYOUT_TOKEN_MAJOR;
   if (!valid_head_size(head_size) || !(valid_block_size(block_size) || (rows && block_size == 1)))
     return fail(PKV_ERR_UNSUPPORTED, "Unsupported head_size/block_size for paged_attention");
+  const bool fp8 = cache_dtype == PKV_FP8_E4M3;
   const bool pair_ok = (q_dtype == PKV_BF16 && cache_dtype == PKV_BF16) ||
                        (q_dtype == PKV_F16 && cache_dtype == PKV_F16) ||
-                       (q_dtype == PKV_F32 && (cache_dtype == PKV_BF16 || cache_dtype == PKV_F16));
+                       (q_dtype == PKV_F32 && (cache_dtype == PKV_BF16 || cache_dtype == PKV_F16)) ||
+                       (fp8 && (q_dtype == PKV_BF16 || q_dtype == PKV_F16 || q_dtype == PKV_F32));
   if (!pair_ok) return fail(PKV_ERR_UNSUPPORTED, "Unsupported query/cache dtype pair for paged_attention");
+  if (fp8 && (rows || head_size % 16 != 0))
+    return fail(PKV_ERR_UNSUPPORTED, "FP8 caches are read in the paged layout with head_size a multiple of 16");
+  if (fp8 && !(std::isfinite(k_scale) && std::isfinite(v_scale) && k_scale != 0.f && v_scale != 0.f))
+    return fail(PKV_ERR_INVALID, "k_scale and v_scale must be finite and nonzero for FP8 caches");
   if (num_blocks <= 0) return fail(PKV_ERR_INVALID, "num_blocks must be positive");
   if (num_seqs == 0) return PKV_OK;
   if (!out || !query || !key_cache || !value_cache || !block_tables || !context_lens)
@@ -224,11 +230,14 @@ int pkv_paged_attention(void* out, const void* query, const void* key_cache, con
   // Token rows: the row stride takes the place of the block stride below.
   const int64_t kbs = rows ? k_block_stride / block_size : k_block_stride;
   const int64_t vbs = rows ? v_block_stride / block_size : v_block_stride;
-  // V: 8-byte loads in the paged layout, 16-byte loads of token rows.
-  const int64_t v_align = rows ? 16 : 8;
-  if (!aligned16(key_cache) || (kbs * 2) % 16 != 0 || (k_head_stride * 2) % 16 != 0 ||
-      (reinterpret_cast<uintptr_t>(value_cache) % v_align) != 0 || (vbs * 2) % v_align != 0 ||
-      (v_head_stride * 2) % v_align != 0)
+  // K: 16-byte loads (8-byte for FP8); V: 8-byte loads in the paged layout
+  // (4-byte for FP8), 16-byte loads of token rows.
+  const int64_t cb = elem_bytes(cache_dtype);
+  const int64_t k_align = fp8 ? 8 : 16;
+  const int64_t v_align = rows ? 16 : fp8 ? 4 : 8;
+  if (!aligned16(key_cache) || (kbs * cb) % k_align != 0 || (k_head_stride * cb) % k_align != 0 ||
+      (reinterpret_cast<uintptr_t>(value_cache) % v_align) != 0 || (vbs * cb) % v_align != 0 ||
+      (v_head_stride * cb) % v_align != 0)
     return fail(PKV_ERR_INVALID, "cache base or strides are not aligned for vector loads");
   const pkv::DecodeWorkspace w = pkv::decode_workspace_layout(num_seqs, num_heads, head_size, parts);
   if (workspace == nullptr || workspace_bytes < w.total)
@@ -252,7 +261,8 @@ int pkv_paged_attention(void* out, const void* query, const void* key_cache, con
   p.k_head_stride = k_head_stride;
   p.v_block_stride = vbs;
   p.v_head_stride = v_head_stride;
-  p.scale_log2 = scale * 1.4426950408889634f;
+  p.scale_log2 = scale * 1.4426950408889634f * (fp8 ? k_scale : 1.f);
+  p.v_scale = fp8 ? v_scale : 1.f;
   p.num_seqs = num_seqs;
   p.num_heads = num_heads;
   p.num_kv_heads = num_kv_heads;
@@ -283,7 +293,14 @@ int pkv_paged_attention(void* out, const void* query, const void* key_cache, con
   bool ok = true;
   hipError_t e = hipErrorInvalidValue;
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  if (q_dtype == PKV_BF16)
+  if (fp8) {
+    if (q_dtype == PKV_BF16)
+      e = pkv::launch_decode_typed<pkv::BF16, pkv::FP8>(p, head_size, block_size, s, &ok);
+    else if (q_dtype == PKV_F16)
+      e = pkv::launch_decode_typed<pkv::F16, pkv::FP8>(p, head_size, block_size, s, &ok);
+    else
+      e = pkv::launch_decode_typed<pkv::F32, pkv::FP8>(p, head_size, block_size, s, &ok);
+  } else if (q_dtype == PKV_BF16)
     e = pkv::launch_decode_typed<pkv::BF16, pkv::BF16>(p, head_size, block_size, s, &ok);
   else if (q_dtype == PKV_F16)
     e = pkv::launch_decode_typed<pkv::F16, pkv::F16>(p, head_size, block_size, s, &ok);

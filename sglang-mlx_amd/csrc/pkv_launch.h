@@ -94,6 +94,9 @@ struct DecodeParams {
   // kernel addresses rows with 32-bit buffer offsets, so it is used only when
   // both fit in 32 bits.
   uint32_t k_rows_bytes, v_rows_bytes;
+  // Output scale: v_scale for FP8 caches (whose k_scale is folded into
+  // scale_log2), 1 otherwise.
+  float v_scale;
 };
 
 // Scratch carve-up shared by the size query and the launcher: per-partition
@@ -124,6 +127,7 @@ int64_t copy_blocks_max_grid_pairs(int64_t block_bytes, bool aligned);
 struct F32;
 struct F16;
 struct BF16;
+struct FP8;
 // Defined in paged_decode_impl.h, instantiated once per (query, cache) type
 // pair in decode_<q>_<cache>.hip.  *ok is cleared for an unsupported
 // head_size / block_size.

@@ -148,14 +148,20 @@ def _check_paged_attention(query, key_cache, value_cache, block_tables, context_
         raise ValueError("Unsupported head_size/block_size for paged_attention")
     # Checks the reference leaves to the kernel.
     qc = _dtype_code(query)
-    cc = _dtype_code(key_cache)
+    try:
+        cc = _FP8_DTYPE_CODE[key_cache.dtype]
+    except KeyError:
+        raise ValueError("Unsupported dtype") from None
     if value_cache.dtype != key_cache.dtype:
         raise ValueError("key_cache and value_cache dtypes differ")
     if not rows and key_cache.shape[4] != 16 // _ELEM_BYTES[key_cache.dtype]:
         raise ValueError("key_cache last dimension must be 16 / element size of the cache dtype")
-    if not (qc == cc and qc != _lib.PKV_F32) and not (qc == _lib.PKV_F32 and cc != _lib.PKV_F32):
+    fp8 = cc == _lib.PKV_FP8_E4M3
+    if not (qc == cc and qc != _lib.PKV_F32) and not (qc == _lib.PKV_F32 and cc != _lib.PKV_F32) and not fp8:
         raise ValueError(
             f"Unsupported query/cache dtype pair for paged_attention: {query.dtype}/{key_cache.dtype}")
+    if fp8 and (rows or query.shape[2] % 16):
+        raise ValueError("FP8 caches are read in the paged layout with head_size a multiple of 16")
     if rows:
         # Rows must be [Hkv, D]-contiguous, and the rows of a block evenly
         # spaced (block stride = block_size * row stride).
@@ -168,13 +174,16 @@ def _check_paged_attention(query, key_cache, value_cache, block_tables, context_
 
 
 def _paged_attention(op, query, key_cache, value_cache, block_tables, context_lens, num_kv_heads,
-                     scale, block_size, max_seq_len, alibi_slopes, partition_size):
+                     scale, block_size, max_seq_len, alibi_slopes, partition_size, k_scale=1.0, v_scale=1.0):
     for t in (query, key_cache, value_cache, block_tables, context_lens):
         _tensor(t)
     _tensor(alibi_slopes, allow_none=True)
     num_kv_heads, block_size, max_seq_len = int(num_kv_heads), int(block_size), int(max_seq_len)
     qc, cc, layout = _check_paged_attention(query, key_cache, value_cache, block_tables, context_lens,
                                             num_kv_heads, block_size, max_seq_len, alibi_slopes)
+    k_scale, v_scale = float(k_scale), float(v_scale)
+    if cc == _lib.PKV_FP8_E4M3 and not all(math.isfinite(v) and v != 0.0 for v in (k_scale, v_scale)):
+        raise ValueError("k_scale and v_scale must be finite and nonzero for FP8 caches")
     _check_index(block_tables)
     _check_index(context_lens)
     dev = _on_gpu(op, query, key_cache, value_cache, block_tables, context_lens, alibi_slopes)
@@ -206,24 +215,26 @@ def _paged_attention(op, query, key_cache, value_cache, block_tables, context_le
             B, Hq, num_kv_heads, D, block_size, bt.shape[1], max_seq_len, key_cache.shape[0],
             float(scale), query.stride(0), key_cache.stride(0), key_cache.stride(-2 if layout else 1),
             value_cache.stride(0), value_cache.stride(-2 if layout else 1), layout, partition_size,
-            ws.data_ptr(), ws.numel(), qc, cc, stream)
+            ws.data_ptr(), ws.numel(), qc, cc, k_scale, v_scale, stream)
     _lib.check(st)
     return out
 
 
 def paged_attention_v1(query, key_cache, value_cache, block_tables, seq_lens, num_kv_heads,
-                       scale, block_size, max_seq_len, alibi_slopes=None):
+                       scale, block_size, max_seq_len, alibi_slopes=None, k_scale=1.0, v_scale=1.0):
     """Single-softmax paged decode attention (bindings.cpp:44-65).
 
     Returns a new tensor shaped and typed like ``query``
-    (mlx_paged_attention.cpp:212).
+    (mlx_paged_attention.cpp:212).  uint8 caches hold FP8 E4M3 codes, read
+    as decode(code) * k_scale / v_scale.
     """
     return _paged_attention("PagedAttentionV1", query, key_cache, value_cache, block_tables, seq_lens,
-                            num_kv_heads, scale, block_size, max_seq_len, alibi_slopes, 0)
+                            num_kv_heads, scale, block_size, max_seq_len, alibi_slopes, 0, k_scale, v_scale)
 
 
 def paged_attention_v2(query, key_cache, value_cache, block_tables, seq_lens, num_kv_heads,
-                       scale, block_size, max_seq_len, alibi_slopes=None, partition_size=512):
+                       scale, block_size, max_seq_len, alibi_slopes=None, partition_size=512, k_scale=1.0,
+                       v_scale=1.0):
     """Split-K paged decode: softmax per partition of ``partition_size``
     tokens, merged across partitions by log-sum-exp.  Same arguments and
     result as ``paged_attention_v1`` plus ``partition_size``."""
@@ -231,7 +242,8 @@ def paged_attention_v2(query, key_cache, value_cache, block_tables, seq_lens, nu
     if partition_size <= 0 or partition_size % 16 or partition_size % int(block_size) or partition_size > 4096:
         raise ValueError("partition_size must be a positive multiple of 16 and of block_size, at most 4096")
     return _paged_attention("PagedAttentionV2", query, key_cache, value_cache, block_tables, seq_lens,
-                            num_kv_heads, scale, block_size, max_seq_len, alibi_slopes, partition_size)
+                            num_kv_heads, scale, block_size, max_seq_len, alibi_slopes, partition_size,
+                            k_scale, v_scale)
 
 
 def _reshape_and_cache(op, key, value, key_cache, value_cache, slot_mapping, flash: bool,

@@ -51,7 +51,8 @@ SIGNATURES = {
         _i64, _i64, _i64, _i64,                                   # k/v block & head strides
         _i32, _i32,                                               # layout, partition_size
         _c_void_p, _size,                                         # workspace, bytes
-        _i32, _i32, _c_void_p,                                    # q dtype, cache dtype, stream
+        _i32, _i32,                                               # q dtype, cache dtype
+        _f32, _f32, _c_void_p,                                    # k_scale, v_scale (FP8), stream
     ]),
     "pkv_copy_blocks": (ctypes.c_int, [
         ctypes.POINTER(_c_void_p), ctypes.POINTER(_c_void_p), _i32,  # src/dst planes, count

@@ -33,6 +33,8 @@ def paged_attention_v1(
     block_size: int,
     max_seq_len: int,
     alibi_slopes: torch.Tensor | None = None,
+    k_scale: float = 1.0,
+    v_scale: float = 1.0,
 ) -> torch.Tensor:
     """Single-pass paged attention (metal_kernels.py:20-61).
 
@@ -47,12 +49,14 @@ def paged_attention_v1(
         block_size: Number of tokens per block
         max_seq_len: Maximum sequence length
         alibi_slopes: Optional ALiBi slopes [num_heads]
+        k_scale, v_scale: for uint8 (FP8 E4M3) caches, K = decode(code) *
+            k_scale and V = decode(code) * v_scale; ignored otherwise
 
     Returns:
         Output tensor [num_seqs, num_heads, head_size], dtype of query.
     """
     return _ext.paged_attention_v1(query, key_cache, value_cache, block_tables, context_lens,
-                                   num_kv_heads, scale, block_size, max_seq_len, alibi_slopes)
+                                   num_kv_heads, scale, block_size, max_seq_len, alibi_slopes, k_scale, v_scale)
 
 
 def paged_attention_v2(
@@ -67,13 +71,15 @@ def paged_attention_v2(
     max_seq_len: int,
     alibi_slopes: torch.Tensor | None = None,
     partition_size: int = 512,
+    k_scale: float = 1.0,
+    v_scale: float = 1.0,
 ) -> torch.Tensor:
     """Split-K paged attention for long contexts: each partition of
     ``partition_size`` tokens yields (max, sum, output); partitions are merged
     by log-sum-exp.  Same arguments and result as ``paged_attention_v1``."""
     return _ext.paged_attention_v2(query, key_cache, value_cache, block_tables, context_lens,
                                    num_kv_heads, scale, block_size, max_seq_len, alibi_slopes,
-                                   partition_size)
+                                   partition_size, k_scale, v_scale)
 
 
 def reshape_and_cache(

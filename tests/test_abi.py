@@ -48,7 +48,7 @@ def attn(**kw):
     a = dict(out=None, q=None, kc=None, vc=None, bt=None, ctx=None, alibi=None, B=2, Hq=8, Hkv=2, D=128, bs=16,
              max_blocks=4, max_seq_len=64, nb=10, scale=1.0, q_stride=1024, kbs=2 * 128 * 16, khs=128 * 16,
              vbs=2 * 128 * 16, vhs=128 * 16, layout=_lib.PKV_LAYOUT_PAGED5D, ps=0, ws=None, ws_bytes=0,
-             qd=_lib.PKV_BF16, cd=_lib.PKV_BF16, stream=None)
+             qd=_lib.PKV_BF16, cd=_lib.PKV_BF16, k_scale=1.0, v_scale=1.0, stream=None)
     a.update(kw)
     lib = _lib.lib()
     st = lib.pkv_paged_attention(*a.values())
@@ -69,6 +69,12 @@ def attn(**kw):
     (dict(bs=32, max_blocks=2, ps=16), 1, "partition_size must be a positive multiple of 16 and of block_size"),
     (dict(nb=0), 1, "num_blocks must be positive"),
     (dict(), 1, "null buffer"),
+    (dict(qd=_lib.PKV_FP8_E4M3, cd=_lib.PKV_FP8_E4M3), 2, "Unsupported query/cache dtype pair"),
+    (dict(cd=_lib.PKV_FP8_E4M3, D=120), 2, "FP8 caches are read in the paged layout"),
+    (dict(cd=_lib.PKV_FP8_E4M3, layout=_lib.PKV_LAYOUT_TOKEN_MAJOR), 2, "FP8 caches are read in the paged layout"),
+    (dict(cd=_lib.PKV_FP8_E4M3, k_scale=float("nan")), 1, "finite and nonzero"),
+    (dict(cd=_lib.PKV_FP8_E4M3, v_scale=0.0), 1, "finite and nonzero"),
+    (dict(cd=_lib.PKV_FP8_E4M3), 1, "null buffer"),
 ])
 def test_paged_attention_rejections(kw, code, msg):
     st, err = attn(**kw)

@@ -133,3 +133,21 @@ def test_convert_fp8_against_torch(src, dst):
         tdt = {"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16}[dst]
         exp = orc.to_storage(v.to(tdt).float().numpy(), dst)
         np.testing.assert_array_equal(got, exp)
+
+
+def test_fp8_cache_attention_is_attention_over_dequantised_caches():
+    # The FP8 branch of the attention oracle equals the pinned float32 path
+    # run on decode(code) * scale.
+    rng = np.random.default_rng(3)
+    B, Hq, Hkv, D, bs, nb = 3, 8, 2, 64, 16, 12
+    kc = orc.fp8_e4m3_encode(rng.standard_normal((nb, Hkv, D // 16, bs, 16)).astype(np.float32) / 0.5)
+    vc = orc.fp8_e4m3_encode(rng.standard_normal((nb, Hkv, D, bs)).astype(np.float32) / 0.25)
+    q = rng.standard_normal((B, Hq, D)).astype(np.float32)
+    bt = rng.permutation(nb)[:B * 4].reshape(B, 4).astype(np.int32)
+    ctx = np.array([1, 37, 64], dtype=np.int32)
+    got = orc.paged_attention(q, kc, vc, bt, ctx, Hkv, 0.125, bs, 64, cache_dtype="fp8_e4m3",
+                              k_scale=0.5, v_scale=0.25)
+    kf = (orc.fp8_e4m3_decode(kc) * np.float32(0.5)).astype(np.float32)
+    vf = (orc.fp8_e4m3_decode(vc) * np.float32(0.25)).astype(np.float32)
+    exp = orc.paged_attention(q, kf, vf, bt, ctx, Hkv, 0.125, bs, 64)
+    np.testing.assert_allclose(got, exp, rtol=1e-12, atol=1e-12)
