@@ -32,11 +32,12 @@ Printed: ONE JSON line with the driver's fields plus
   token_rows    the decode layer on token-row caches: MHATokenPool's
                 [rows, Hkv, D] buffer through slot tables (block size 1) and
                 the flash layout [blocks, 16, Hkv, D];
+  fp8_kv        the decode layer over FP8 E4M3 caches (half the KV bytes);
   cpu_baseline  the reference's gather + SDPA decode restated in torch on
                 this host's cores, on the same inputs (full batch, one layer).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-append] [--no-splitk] [--no-radix]
-                       [--no-rows] [--only LEG]
+                       [--no-rows] [--no-fp8] [--only LEG]
 """
 
 from __future__ import annotations
@@ -73,7 +74,8 @@ def parse_args():
     ap.add_argument("--no-splitk", action="store_true", help="skip the long-context split-K measurement")
     ap.add_argument("--no-radix", action="store_true", help="skip the radix-shared decode measurement")
     ap.add_argument("--no-rows", action="store_true", help="skip the token-row (MHATokenPool) decode measurement")
-    ap.add_argument("--only", choices=["decode", "append", "copy", "splitk", "radix", "rows"],
+    ap.add_argument("--no-fp8", action="store_true", help="skip the FP8-cache decode measurement")
+    ap.add_argument("--only", choices=["decode", "append", "copy", "splitk", "radix", "rows", "fp8"],
                     help="run one leg and print its own short JSON line (for counter collection under "
                          "rocprofv3 --pmc): the decode layer, the token-major append, or a plain 1 GiB device "
                          "copy whose FETCH_SIZE / WRITE_SIZE calibrate the counters")
@@ -268,6 +270,53 @@ def bench_rows(dev, kernels, layers: int = 4, steps: int = 100, warmup: int = 10
         torch.cuda.empty_cache()
     out["kernel"] = "paged_decode_persist_kernel<BF16, BF16, 128, 0> (token-row mode)"
     out["timing"] = f"HIP events around {steps} back-to-back launches after {warmup} warm-up launches"
+    return out
+
+
+def bench_fp8(dev, kernels, layers: int = 4, steps: int = 100, warmup: int = 10):
+    """The Llama-3-8B decode layer of bench_decode (same sequences, context
+    lengths and block tables) over FP8 E4M3 caches (paged 5-D, x = 16) with
+    k_scale / v_scale: half the KV bytes.  Layer pools rotated."""
+    B, Hq, Hkv, D, bs = 64, 32, 8, 128, 16
+    rng = np.random.default_rng(1003)
+    ctx = rng.integers(512, 4096 + 1, size=B).astype(np.int64)
+    nblk = -(-ctx // bs)
+    nb = int(math.ceil(int(nblk.sum()) * 1.1)) + 1
+    perm = rng.permutation(np.arange(1, nb))
+    bt = np.full((B, -(-4096 // bs)), -1, dtype=np.int32)
+    pos = 0
+    for s in range(B):
+        bt[s, :nblk[s]] = perm[pos:pos + nblk[s]]
+        pos += nblk[s]
+    g = torch.Generator(device=dev)
+    g.manual_seed(1003)
+    q = torch.randn((B, Hq, D), generator=g, device=dev).to(torch.bfloat16)
+    k_scale, v_scale = 0.05, 0.02
+    pools = []
+    for _ in range(layers):
+        kc = torch.empty((nb, Hkv, D // 16, bs, 16), dtype=torch.uint8, device=dev)
+        vc = torch.empty((nb, Hkv, D, bs), dtype=torch.uint8, device=dev)
+        kernels.convert_fp8(kc, torch.randn(kc.shape, generator=g, device=dev) * 1.5, k_scale * 20.0)
+        kernels.convert_fp8(vc, torch.randn(vc.shape, generator=g, device=dev) * 0.5, v_scale * 20.0)
+        pools.append((kc, vc))
+    btd = torch.from_numpy(bt).to(dev)
+    lens = torch.from_numpy(ctx.astype(np.int32)).to(dev)
+    scale = 1.0 / math.sqrt(D)
+
+    def step(i):
+        kc, vc = pools[i % layers]
+        kernels.paged_attention_v1(q, kc, vc, btd, lens, Hkv, scale, bs, 4096, k_scale=k_scale, v_scale=v_scale)
+
+    _, dev_s = timed_launches(step, steps, warmup)
+    us = dev_s * 1e6 / steps
+    nbytes = decode_bytes(ctx, B, Hq, Hkv, D, bs, s_kv=1)
+    gbs = nbytes / (us * 1e-6) / 1e9
+    out = dict(us=round(us, 2), bytes_per_launch=nbytes, gbs=round(gbs, 1), frac=round(gbs / PEAK_GBS, 4),
+               kernel="paged_decode_persist_kernel<BF16, FP8, 128, 16>",
+               cache="E4M3 (reference format), x = 16, k_scale 0.05, v_scale 0.02",
+               timing=f"HIP events around {steps} back-to-back launches after {warmup} warm-up launches")
+    del pools
+    torch.cuda.empty_cache()
     return out
 
 
@@ -471,6 +520,8 @@ def only_leg(args, dev, kernels):
         print(json.dumps(dict(leg="radix", **bench_radix(dev, kernels))))
     elif args.only == "rows":
         print(json.dumps(dict(leg="rows", **bench_rows(dev, kernels))))
+    elif args.only == "fp8":
+        print(json.dumps(dict(leg="fp8", **bench_fp8(dev, kernels))))
     else:
         n = 1 << 30
         src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
@@ -548,6 +599,8 @@ def main():
         line["radix_shared"] = bench_radix(dev, kernels)
     if not args.no_rows:
         line["token_rows"] = bench_rows(dev, kernels)
+    if not args.no_fp8:
+        line["fp8_kv"] = bench_fp8(dev, kernels)
     if not args.no_cpu:
         line["cpu_baseline"] = bench_cpu(res, args.cpu_budget)
     else:

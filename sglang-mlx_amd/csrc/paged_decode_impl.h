@@ -1124,12 +1124,15 @@ __global__ __launch_bounds__(64 * kPartWaves) void paged_decode_rows_kernel(Deco
 #ifndef PKV_ROWS_NBUF
 #define PKV_ROWS_NBUF 2
 #endif
-template <int D, bool ROWS = false> struct Persist {
+#ifndef PKV_FP8_NBUF
+#define PKV_FP8_NBUF 2
+#endif
+template <int D, bool ROWS = false, bool F8 = false> struct Persist {
   // Wavefronts per workgroup: two per SIMD while the register budget allows
   // (head sizes up to 128), one above.
   static constexpr int kWaves = D <= 128 ? (ROWS ? PKV_ROWS_WAVES : 8) : 4;
   // Tile buffers per wavefront.
-  static constexpr int kMaxBuf = ROWS ? PKV_ROWS_NBUF : 2;
+  static constexpr int kMaxBuf = ROWS ? PKV_ROWS_NBUF : F8 ? PKV_FP8_NBUF : 2;
 };
 
 struct PersistItem {
@@ -1249,7 +1252,7 @@ __global__ __launch_bounds__(64 * (Persist<D, BS == 0>::kWaves)) void paged_deco
         blk.kr = __builtin_amdgcn_make_buffer_rsrc((void*)kbase, (short)0, (int)p.k_rows_bytes, kBufferRsrcWord3);
         blk.vr = __builtin_amdgcn_make_buffer_rsrc((void*)vbase, (short)0, (int)p.v_rows_bytes, kBufferRsrcWord3);
       }
-      stream_tiles<QT, CT, D, TBS, NW, MAXT, Persist<D, ROWS>::kMaxBuf, ROWS, Blocks>(p, kbase, vbase, blk, 0, (int)it.ctx, it.ctx, wave, g,
+      stream_tiles<QT, CT, D, TBS, NW, MAXT, Persist<D, ROWS, std::is_same<CT, FP8>::value>::kMaxBuf, ROWS, Blocks>(p, kbase, vbase, blk, 0, (int)it.ctx, it.ctx, wave, g,
                                                               col, qa, qb, slope, acc);
     }
     // Every wavefront reads s_red[buf] right after this item's barrier and
