@@ -607,6 +607,145 @@ __device__ __forceinline__ void load_query(const DecodeParams& p, int seq, int h
   }
 }
 
+// Consumes one loaded tile of tokens tt0 .. tt0+15 into acc.  TAIL: the tile
+// crosses t1, so tokens at or past t1 are masked.  Tokens of masked-out
+// blocks contribute nothing either.  Masked tokens get score -inf and V zero
+// (a slot may hold anything, including NaN); with block_size >= 16 a masked
+// block's loads already returned zero, so only its scores need masking.
+// ctx is the context length of the lane's column (its ALiBi origin).
+// COLMASK: columns with col_on false take no part in this tile (their
+// scores are -inf), for tiles that serve only some of the columns.
+template <class QT, class CT, int D, int BS, bool ROWS, bool TAIL, bool COLMASK = false>
+__device__ __forceinline__ void consume_tile(const DecodeParams& p, Tile<D, std::is_same<CT, FP8>::value>& t,
+                                             int tt0, int t1, uint32_t ctx, int g, int col,
+                                             const uint4 (&qa)[Tile<D>::KSTEPS],
+                                             const uint4 (&qb)[std::is_same<QT, F32>::value ? Tile<D>::KSTEPS : 1],
+                                             float slope, WaveAcc<D>& acc, bool col_on = true) {
+  constexpr int KSTEPS = Tile<D>::KSTEPS;
+  constexpr int DT = Tile<D>::DT;
+  constexpr bool SPLIT_Q = std::is_same<QT, F32>::value;
+  constexpr bool F8 = std::is_same<CT, FP8>::value;
+  using MT = typename MmaOf<QT, CT>::type;
+  const int vtok = tt0 + 4 * g;
+  if constexpr (F8) dequant_tile<MT, D>(t);
+  if constexpr (ROWS) transpose_tile_rows<D>(t, col);
+  bool zero_v = false;
+  if constexpr (TAIL) {
+    zero_v = true;
+  } else if constexpr (ROWS || BS < kTile) {
+    zero_v = !__all(t.vpb >= 0 && t.kpb >= 0);
+  }
+  if (zero_v) {
+    uint32_t m01, m23;
+    if constexpr (ROWS) {
+      // Token rows: V tokens 4g .. 4g+3 are valid where their (shared) K
+      // row is, which lane 4g + r of this row group holds.
+      const bool v0 = vtok + 0 < t1 && __shfl(t.kpb, 4 * g + 0, 16) >= 0;
+      const bool v1 = vtok + 1 < t1 && __shfl(t.kpb, 4 * g + 1, 16) >= 0;
+      const bool v2 = vtok + 2 < t1 && __shfl(t.kpb, 4 * g + 2, 16) >= 0;
+      const bool v3 = vtok + 3 < t1 && __shfl(t.kpb, 4 * g + 3, 16) >= 0;
+      m01 = (v0 ? 0x0000ffffu : 0u) | (v1 ? 0xffff0000u : 0u);
+      m23 = (v2 ? 0x0000ffffu : 0u) | (v3 ? 0xffff0000u : 0u);
+    } else {
+      const uint32_t ok = t.vpb >= 0 ? 0xffffffffu : 0u;
+      m01 = ok & ((vtok + 0 < t1 ? 0x0000ffffu : 0u) | (vtok + 1 < t1 ? 0xffff0000u : 0u));
+      m23 = ok & ((vtok + 2 < t1 ? 0x0000ffffu : 0u) | (vtok + 3 < t1 ? 0xffff0000u : 0u));
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      t.v[dt].x &= m01;
+      t.v[dt].y &= m23;
+    }
+  }
+  // ---- S^T = K * Q^T ----
+  f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < KSTEPS; ++j) {
+    sacc = Mma<MT>::k32(t.k[j], qa[j], sacc);
+    if constexpr (SPLIT_Q) sacc = Mma<MT>::k32(t.k[j], qb[j], sacc);
+  }
+  // ---- online softmax (log2 domain) ----
+  float sc[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) sc[r] = sacc[r] * p.scale_log2;
+  if (p.alibi != nullptr) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sc[r] += slope * (float)(vtok + r - (int)ctx + 1);
+  }
+  if constexpr (COLMASK) {
+    if (!col_on) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sc[r] = -INFINITY;
+    }
+  }
+  if (TAIL || zero_v) {
+    // Lane (g, col) holds scores of tokens vtok..vtok+3 for head col; the K
+    // row of token tt0 + i was loaded by lane col = i.
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int krow_ok = __shfl(t.kpb, 4 * g + r, 16) >= 0;
+      sc[r] = (vtok + r < t1 && t.vpb >= 0 && krow_ok) ? sc[r] : -INFINITY;
+    }
+  } else if constexpr (BS >= kTile) {
+    if (t.vpb < 0) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sc[r] = -INFINITY;
+    }
+  }
+  const float mt = column_max(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
+  acc.m_max = fmaxf(acc.m_max, mt);
+  if (__any(mt > acc.m_run + kRescaleSlack)) {
+    const float m_new = fmaxf(acc.m_run, mt);
+    const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(acc.m_run - m_new);
+    acc.l_run *= alpha;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) acc.o[dt] *= alpha;
+    acc.m_run = m_new;
+  }
+  const float m_use = acc.m_run == -INFINITY ? 0.f : acc.m_run;
+  float pr[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) pr[r] = fast_exp2(sc[r] - m_use);
+  acc.l_run += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+  // ---- O^T += V^T * P^T ----
+  const uint2 pp = make_uint2(pack_p<MT>(pr[0], pr[1]), pack_p<MT>(pr[2], pr[3]));
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) acc.o[dt] = Mma<MT>::k16(t.v[dt], pp, acc.o[dt]);
+}
+
+// load_query with the lane's own sequence and query head (columns of one
+// MFMA serving several sequences); inactive lanes get zeros.
+template <class QT, class CT, int D>
+__device__ __forceinline__ void load_query_lane(const DecodeParams& p, int seq, int head, bool active, int g,
+                                                uint4 (&qa)[Tile<D>::KSTEPS],
+                                                uint4 (&qb)[std::is_same<QT, F32>::value ? Tile<D>::KSTEPS : 1]) {
+  using QS = typename Elem<QT>::storage;
+  constexpr bool SPLIT_Q = std::is_same<QT, F32>::value;
+  const QS* qrow = static_cast<const QS*>(p.q) + (int64_t)(active ? seq : 0) * p.q_stride +
+                   (int64_t)(active ? head : 0) * D;
+#pragma unroll
+  for (int j = 0; j < Tile<D>::KSTEPS; ++j) {
+    const int d0 = 32 * j + 8 * g;
+    uint4 a = make_uint4(0, 0, 0, 0), b = make_uint4(0, 0, 0, 0);
+    if (active && d0 < D) {
+      if constexpr (SPLIT_Q) {
+        const float4 x0 = *reinterpret_cast<const float4*>(qrow + d0);
+        const float4 x1 = *reinterpret_cast<const float4*>(qrow + d0 + 4);
+        const float x[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        uint32_t h[8], l[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) split_q<CT>(x[e], h[e], l[e]);
+        a = make_uint4(pack2(h[0], h[1]), pack2(h[2], h[3]), pack2(h[4], h[5]), pack2(h[6], h[7]));
+        b = make_uint4(pack2(l[0], l[1]), pack2(l[2], l[3]), pack2(l[4], l[5]), pack2(l[6], l[7]));
+      } else {
+        a = *reinterpret_cast<const uint4*>(qrow + d0);
+      }
+    }
+    qa[j] = a;
+    if constexpr (SPLIT_Q) qb[j] = b;
+  }
+}
+
 // Streams the 16-token tiles first, first+NW, ... of tokens [t0, t1) of one
 // (sequence, KV head) through the online softmax into acc.  blk holds the
 // wavefront's block ids (WaveBlocks::load with the same first, NW, t0);
@@ -626,10 +765,8 @@ __device__ __forceinline__ void stream_tiles(const DecodeParams& p, const typena
                                              float slope, WaveAcc<D>& acc) {
   constexpr int KSTEPS = Tile<D>::KSTEPS;
   constexpr int DT = Tile<D>::DT;
-  constexpr bool SPLIT_Q = std::is_same<QT, F32>::value;
   constexpr int PT = WaveBlocks<BS, MAXT>::PER_TILE;
   constexpr bool F8 = std::is_same<CT, FP8>::value;
-  using MT = typename MmaOf<QT, CT>::type;
   using TileT = Tile<D, F8>;
   const int ntiles = (t1 - t0 + kTile - 1) / kTile;
   const int nfull = (t1 - t0) / kTile;  // tiles entirely inside [t0, t1)
@@ -648,92 +785,8 @@ __device__ __forceinline__ void stream_tiles(const DecodeParams& p, const typena
   // expcnt 6:4 and lgkmcnt 11:8 left at their maxima (no wait).
   constexpr int kWaitAhead = (AHEAD & 15) | ((AHEAD >> 4) << 14) | (7 << 4) | (15 << 8);
 
-  // Consumes one loaded tile starting at token tt0.  TAIL: the tile crosses
-  // t1, so tokens at or past t1 are masked.  Tokens of masked-out blocks
-  // contribute nothing either.  Masked tokens get score -inf and V zero (a
-  // slot may hold anything, including NaN); with block_size >= 16 a masked
-  // block's loads already returned zero, so only its scores need masking.
   auto consume = [&](auto tail_tag, TileT& t, int tt0) {
-    constexpr bool TAIL = decltype(tail_tag)::value;
-    const int vtok = tt0 + 4 * g;
-    if constexpr (F8) dequant_tile<MT, D>(t);
-    if constexpr (ROWS) transpose_tile_rows<D>(t, col);
-    bool zero_v = false;
-    if constexpr (TAIL) {
-      zero_v = true;
-    } else if constexpr (ROWS || BS < kTile) {
-      zero_v = !__all(t.vpb >= 0 && t.kpb >= 0);
-    }
-    if (zero_v) {
-      uint32_t m01, m23;
-      if constexpr (ROWS) {
-        // Token rows: V tokens 4g .. 4g+3 are valid where their (shared) K
-        // row is, which lane 4g + r of this row group holds.
-        const bool v0 = vtok + 0 < t1 && __shfl(t.kpb, 4 * g + 0, 16) >= 0;
-        const bool v1 = vtok + 1 < t1 && __shfl(t.kpb, 4 * g + 1, 16) >= 0;
-        const bool v2 = vtok + 2 < t1 && __shfl(t.kpb, 4 * g + 2, 16) >= 0;
-        const bool v3 = vtok + 3 < t1 && __shfl(t.kpb, 4 * g + 3, 16) >= 0;
-        m01 = (v0 ? 0x0000ffffu : 0u) | (v1 ? 0xffff0000u : 0u);
-        m23 = (v2 ? 0x0000ffffu : 0u) | (v3 ? 0xffff0000u : 0u);
-      } else {
-        const uint32_t ok = t.vpb >= 0 ? 0xffffffffu : 0u;
-        m01 = ok & ((vtok + 0 < t1 ? 0x0000ffffu : 0u) | (vtok + 1 < t1 ? 0xffff0000u : 0u));
-        m23 = ok & ((vtok + 2 < t1 ? 0x0000ffffu : 0u) | (vtok + 3 < t1 ? 0xffff0000u : 0u));
-      }
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        t.v[dt].x &= m01;
-        t.v[dt].y &= m23;
-      }
-    }
-    // ---- S^T = K * Q^T ----
-    f32x4 sacc = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int j = 0; j < KSTEPS; ++j) {
-      sacc = Mma<MT>::k32(t.k[j], qa[j], sacc);
-      if constexpr (SPLIT_Q) sacc = Mma<MT>::k32(t.k[j], qb[j], sacc);
-    }
-    // ---- online softmax (log2 domain) ----
-    float sc[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) sc[r] = sacc[r] * p.scale_log2;
-    if (p.alibi != nullptr) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) sc[r] += slope * (float)(vtok + r - (int)ctx + 1);
-    }
-    if (TAIL || zero_v) {
-      // Lane (g, col) holds scores of tokens vtok..vtok+3 for head col; the K
-      // row of token tt0 + i was loaded by lane col = i.
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int krow_ok = __shfl(t.kpb, 4 * g + r, 16) >= 0;
-        sc[r] = (vtok + r < t1 && t.vpb >= 0 && krow_ok) ? sc[r] : -INFINITY;
-      }
-    } else if constexpr (BS >= kTile) {
-      if (t.vpb < 0) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) sc[r] = -INFINITY;
-      }
-    }
-    const float mt = column_max(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
-    acc.m_max = fmaxf(acc.m_max, mt);
-    if (__any(mt > acc.m_run + kRescaleSlack)) {
-      const float m_new = fmaxf(acc.m_run, mt);
-      const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(acc.m_run - m_new);
-      acc.l_run *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) acc.o[dt] *= alpha;
-      acc.m_run = m_new;
-    }
-    const float m_use = acc.m_run == -INFINITY ? 0.f : acc.m_run;
-    float pr[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) pr[r] = fast_exp2(sc[r] - m_use);
-    acc.l_run += (pr[0] + pr[1]) + (pr[2] + pr[3]);
-    // ---- O^T += V^T * P^T ----
-    const uint2 pp = make_uint2(pack_p<MT>(pr[0], pr[1]), pack_p<MT>(pr[2], pr[3]));
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) acc.o[dt] = Mma<MT>::k16(t.v[dt], pp, acc.o[dt]);
+    consume_tile<QT, CT, D, BS, ROWS, decltype(tail_tag)::value>(p, t, tt0, t1, ctx, g, col, qa, qb, slope, acc);
   };
   using Full = std::integral_constant<bool, false>;
   using Tail = std::integral_constant<bool, true>;
@@ -872,11 +925,13 @@ __device__ __forceinline__ void store4(typename Elem<QT>::storage* dst, float a,
 // loads ahead of its output stores and it would start that item late.)
 // The weights and sums follow the same order as merge_waves, so the result
 // is the reference's sum(exp(s - max) v) / (sum(exp(s - max)) + 1e-6).
+// hrow: the output row of the lane's column; active: whether the column
+// has one.
 template <class QT, int D, int NW, bool ROWS = false>
 __device__ __forceinline__ void merge_store_waves(const DecodeParams& p, WaveAcc<D>& acc,
                                                   float4 (*s_red)[Tile<D>::DT][64], float (*s_m)[16],
-                                                  float (*s_l)[16], int wave, int lane, int g, int col, int64_t hrow0,
-                                                  int nh) {
+                                                  float (*s_l)[16], int wave, int lane, int g, int col, int64_t hrow,
+                                                  bool active) {
   using QS = typename Elem<QT>::storage;
   constexpr int DT = Tile<D>::DT;
   if (acc.m_max != -INFINITY && acc.m_max != acc.m_run) {
@@ -895,7 +950,7 @@ __device__ __forceinline__ void merge_store_waves(const DecodeParams& p, WaveAcc
     s_l[wave][col] = l_col;
   }
   __syncthreads();
-  if (col >= nh) return;
+  if (!active) return;
   float M = s_m[0][col];
 #pragma unroll
   for (int w = 1; w < NW; ++w) M = fmaxf(M, s_m[w][col]);
@@ -908,7 +963,7 @@ __device__ __forceinline__ void merge_store_waves(const DecodeParams& p, WaveAcc
     L += s_l[w][col] * aw[w];
   }
   const float inv = p.v_scale / (L + 1e-6f);
-  QS* out = static_cast<QS*>(p.out) + (hrow0 + col) * D;
+  QS* out = static_cast<QS*>(p.out) + hrow * D;
   for (int dt = wave; dt < DT; dt += NW) {
     const int d0 = tile_dim<D, ROWS>(dt, g);
     if (D % 16 != 0 && d0 >= D) continue;  // head sizes are multiples of 8
@@ -1135,6 +1190,32 @@ template <int D, bool ROWS = false, bool F8 = false> struct Persist {
   static constexpr int kMaxBuf = ROWS ? PKV_ROWS_NBUF : F8 ? PKV_FP8_NBUF : 2;
 };
 
+// Longest-first rank of the sequences (ties by index) into s_order, when
+// there are at most kPersistMaxOrder of them (returns whether it did).
+// Empty and over-long contexts (zero rows) count as length 0.  Every thread
+// of the workgroup calls it.
+__device__ __forceinline__ bool rank_sequences(const DecodeParams& p, uint32_t* s_ctx, int32_t* s_order, int tid,
+                                               int nt) {
+  const int B = p.num_seqs;
+  if (B > kPersistMaxOrder) return false;
+  for (int s = tid; s < B; s += nt) {
+    const uint32_t c = (uint32_t)p.context_lens[s];
+    s_ctx[s] = c > (uint32_t)p.max_seq_len ? 0u : c;
+  }
+  __syncthreads();
+  for (int s = tid; s < B; s += nt) {
+    const uint32_t c = s_ctx[s];
+    int r = 0;
+    for (int s2 = 0; s2 < B; ++s2) {
+      const uint32_t c2 = s_ctx[s2];
+      r += (c2 > c) || (c2 == c && s2 < s);
+    }
+    s_order[r] = s;
+  }
+  __syncthreads();
+  return true;
+}
+
 struct PersistItem {
   int seq, kvh, h0, nh;
   uint32_t ctx;
@@ -1169,26 +1250,7 @@ __global__ __launch_bounds__(64 * (Persist<D, BS == 0>::kWaves)) void paged_deco
   const int total = B * p.units;
   const int G = gridDim.x;
 
-  // Longest-first rank of the sequences (ties by index).  Empty and
-  // over-long contexts (zero rows) count as length 0.
-  const bool ordered = B <= kPersistMaxOrder;
-  if (ordered) {
-    for (int s = tid; s < B; s += NT) {
-      const uint32_t c = (uint32_t)p.context_lens[s];
-      s_ctx[s] = c > (uint32_t)p.max_seq_len ? 0u : c;
-    }
-    __syncthreads();
-    for (int s = tid; s < B; s += NT) {
-      const uint32_t c = s_ctx[s];
-      int r = 0;
-      for (int s2 = 0; s2 < B; ++s2) {
-        const uint32_t c2 = s_ctx[s2];
-        r += (c2 > c) || (c2 == c && s2 < s);
-      }
-      s_order[r] = s;
-    }
-    __syncthreads();
-  }
+  const bool ordered = rank_sequences(p, s_ctx, s_order, tid, NT);
   // Rank of this workgroup's k-th item (>= total: none).
   auto rank_of = [&](int k) { return k * G + ((k & 1) ? G - 1 - (int)blockIdx.x : (int)blockIdx.x); };
   auto item_at = [&](int rank) {
@@ -1259,10 +1321,272 @@ __global__ __launch_bounds__(64 * (Persist<D, BS == 0>::kWaves)) void paged_deco
     // before it reaches the next item's; s_red[buf] is written again only
     // after that one, two items later.
     merge_store_waves<QT, D, NW, ROWS>(p, acc, s_red[buf], s_m[buf], s_l[buf], wave, lane, g, col,
-                                 (int64_t)it.seq * p.num_heads + it.h0, it.nh);
+                                       (int64_t)it.seq * p.num_heads + it.h0 + col, col < it.nh);
     if (!has_next) break;
     it = nit;
     blk = nblk;
+#pragma unroll
+    for (int j = 0; j < KSTEPS; ++j) qa[j] = nqa[j];
+    if constexpr (SPLIT_Q) {
+#pragma unroll
+      for (int j = 0; j < KSTEPS; ++j) qb[j] = nqb[j];
+    }
+    slope = nslope;
+    buf ^= 1;
+    ++k;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Grouped persistent kernel (paged layout): each item is (S sequences of
+// neighbouring rank, KV head), and the 16 MFMA columns hold the GQA query
+// heads of all S sequences (S * group <= 16).  A wavefront walks its tiles
+// w, w+NW, ... of the longest of the S contexts; tile by tile:
+//   * shared -- every live sequence of the item maps the tile to the same
+//     block(s) and holds all 16 of its tokens: the tile is loaded once and
+//     feeds all columns (a radix-shared prefix is read once per S sequences);
+//   * otherwise each sequence whose context reaches the tile gets it as a
+//     job of its own, with only its columns active.
+// Jobs are streamed through two tile buffers, the next job's loads issued
+// before the current one is consumed, so shared and private tiles follow
+// each other without a pipeline refill.  A tile is never loaded more often
+// than by the one-sequence kernels, and the MFMA count per loaded tile is the
+// same; what sharing saves is loads.  Items are ranked and dealt like the
+// persistent kernel's (groups of S sequences in longest-first order).
+// ---------------------------------------------------------------------------
+constexpr int kGroupSeqs = 4;       // sequences per item
+constexpr int kGroupMaxSeq = 8192;  // longest context (block ids in registers)
+
+template <int S> struct GroupItem {
+  int kvh;
+  int seq[S];       // -1: no sequence in this slot (last, partial group)
+  uint32_t ctx[S];  // 0 unless live
+};
+
+template <class QT, class CT, int D, int BS, int S>
+__global__ __launch_bounds__(64 * Persist<D>::kWaves) void paged_decode_group_kernel(DecodeParams p) {
+  constexpr int NW = Persist<D>::kWaves;
+  constexpr int NT = 64 * NW;
+  constexpr int KSTEPS = Tile<D>::KSTEPS;
+  constexpr int DT = Tile<D>::DT;
+  constexpr bool SPLIT_Q = std::is_same<QT, F32>::value;
+  constexpr bool F8 = std::is_same<CT, FP8>::value;
+  constexpr int MAXT = kGroupMaxSeq / kTile / NW;  // tiles per wavefront
+  using Blocks = WaveBlocks<BS, MAXT>;
+  constexpr int PT = Blocks::PER_TILE;
+  using TileT = Tile<D, F8>;
+  using CS = typename Elem<CT>::storage;
+  using MT = typename MmaOf<QT, CT>::type;
+  constexpr int LOADS = KSTEPS + DT;
+  static_assert(LOADS < 64, "vmcnt counts at most 63 outstanding loads");
+  constexpr int kWaitAhead = (LOADS & 15) | ((LOADS >> 4) << 14) | (7 << 4) | (15 << 8);
+
+  __shared__ float4 s_red[2][NW][DT][64];
+  __shared__ float s_m[2][NW][16];
+  __shared__ float s_l[2][NW][16];
+  __shared__ uint32_t s_ctx[kPersistMaxOrder];
+  __shared__ int32_t s_order[kPersistMaxOrder];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, col = lane & 15;
+  const int B = p.num_seqs;
+  const int grp = p.group;  // query heads per KV head; S * grp <= 16 (checked by the launcher)
+  const int ngroups = (B + S - 1) / S;
+  const int total = ngroups * p.num_kv_heads;
+  const int G = gridDim.x;
+  // The lane's column: sequence slot ci of the item, query head hc of its group.
+  const int ci = col / grp;
+  const int hc = col - ci * grp;
+  const bool col_used = ci < S;
+
+  const bool ordered = rank_sequences(p, s_ctx, s_order, tid, NT);
+  auto rank_of = [&](int k) { return k * G + ((k & 1) ? G - 1 - (int)blockIdx.x : (int)blockIdx.x); };
+  auto item_at = [&](int rank, GroupItem<S>& it) {
+    const int gr = rank / p.num_kv_heads;
+    it.kvh = rank - gr * p.num_kv_heads;
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+      const int sr = gr * S + i;
+      it.seq[i] = sr < B ? (ordered ? s_order[sr] : sr) : -1;
+      const uint32_t c = it.seq[i] >= 0 ? (uint32_t)p.context_lens[it.seq[i]] : 0u;
+      it.ctx[i] = (c != 0 && c <= (uint32_t)p.max_seq_len) ? c : 0u;
+    }
+  };
+  const int nlb_max = (p.max_seq_len + BS - 1) / BS;
+  auto load_blocks = [&](const GroupItem<S>& it, Blocks (&blk)[S]) {
+#pragma unroll
+    for (int i = 0; i < S; ++i)
+      blk[i].load(p.block_tables + (int64_t)(it.seq[i] >= 0 ? it.seq[i] : 0) * p.max_blocks_per_seq, p.num_blocks,
+                  nlb_max, 0, 0, wave, NW, lane);
+  };
+  // Per-lane view of the item: the column's sequence, context and slope.
+  auto lane_of = [&](const GroupItem<S>& it, int& seq, uint32_t& ctx) {
+    seq = -1;
+    ctx = 0;
+#pragma unroll
+    for (int i = 0; i < S; ++i)
+      if (ci == i) {
+        seq = it.seq[i];
+        ctx = it.ctx[i];
+      }
+  };
+  auto load_lane_query = [&](const GroupItem<S>& it, uint4 (&qa)[KSTEPS], uint4 (&qb)[SPLIT_Q ? KSTEPS : 1],
+                             float& slope) {
+    int seq;
+    uint32_t ctx;
+    lane_of(it, seq, ctx);
+    const bool on = col_used && seq >= 0;
+    const int head = it.kvh * grp + hc;
+    load_query_lane<QT, MT, D>(p, seq, head, on, g, qa, qb);
+    slope = (p.alibi != nullptr && on) ? p.alibi[head] * kLog2e : 0.f;
+  };
+
+  int k = 0;
+  const int rank = rank_of(0);
+  if (rank >= total) return;
+  GroupItem<S> it;
+  item_at(rank, it);
+  Blocks blk[S];
+  load_blocks(it, blk);
+  uint4 qa[KSTEPS];
+  uint4 qb[SPLIT_Q ? KSTEPS : 1];
+  float slope;
+  load_lane_query(it, qa, qb, slope);
+
+  int buf = 0;
+  while (true) {
+    const int nrank = rank_of(k + 1);
+    const bool has_next = nrank < total;
+    GroupItem<S> nit = it;
+    Blocks nblk[S];
+    uint4 nqa[KSTEPS];
+    uint4 nqb[SPLIT_Q ? KSTEPS : 1];
+    float nslope = 0.f;
+    if (has_next) {
+      item_at(nrank, nit);
+      load_blocks(nit, nblk);
+      load_lane_query(nit, nqa, nqb, nslope);
+    }
+
+    // ---- the item's jobs ----
+    int nt[S];  // tiles per sequence (0: not live)
+    int maxnt = 0;
+    uint32_t minctx = 0xffffffffu;
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+      nt[i] = ((int)it.ctx[i] + kTile - 1) / kTile;
+      maxnt = max(maxnt, nt[i]);
+      if (it.ctx[i] != 0) minctx = min(minctx, it.ctx[i]);
+    }
+    int lane_seq;
+    uint32_t lane_ctx;
+    lane_of(it, lane_seq, lane_ctx);
+    const bool lane_live = col_used && lane_ctx != 0;
+    const CS* kbase = static_cast<const CS*>(p.k_cache) + (int64_t)it.kvh * p.k_head_stride;
+    const CS* vbase = static_cast<const CS*>(p.v_cache) + (int64_t)it.kvh * p.v_head_stride;
+
+    // Job = (tile index k of this wavefront, sequence slot i, or -1 for a
+    // shared tile); kk < 0 marks the end.  All wave-uniform.
+    struct Job {
+      int kk, i;
+    };
+    auto block_of = [&](int i, int e) {
+      int b = blk[0].get(e);
+#pragma unroll
+      for (int s2 = 1; s2 < S; ++s2)
+        if (i == s2) b = blk[s2].get(e);
+      return b;
+    };
+    auto job_at_tile = [&](int kk) -> Job {
+      const int tile = wave + kk * NW;
+      if (tile >= maxnt) return Job{-1, 0};
+      bool shared = (uint32_t)(tile + 1) * kTile <= minctx;
+      int first_live = -1, b0 = 0, b1 = 0;
+#pragma unroll
+      for (int i = 0; i < S; ++i) {
+        if (it.ctx[i] == 0) continue;
+        const int c0 = block_of(i, kk * PT), c1 = PT == 2 ? block_of(i, kk * PT + 1) : c0;
+        if (first_live < 0) {
+          first_live = i;
+          b0 = c0;
+          b1 = c1;
+        } else {
+          shared = shared && c0 == b0 && c1 == b1;
+        }
+      }
+      if (shared) return Job{kk, -1};
+#pragma unroll
+      for (int i = 0; i < S; ++i)
+        if (tile < nt[i]) return Job{kk, i};
+      return Job{-1, 0};  // not reached: tile < maxnt
+    };
+    auto next_job = [&](Job j) -> Job {
+      if (j.i >= 0) {
+        const int tile = wave + j.kk * NW;
+#pragma unroll
+        for (int i = 0; i < S; ++i)
+          if (i > j.i && tile < nt[i]) return Job{j.kk, i};
+      }
+      return job_at_tile(j.kk + 1);
+    };
+    auto load_job = [&](TileT& t, Job j) {
+      const int sel = j.i >= 0 ? j.i : [&] {
+        int f = 0;
+#pragma unroll
+        for (int i = S - 1; i >= 0; --i)
+          if (it.ctx[i] != 0) f = i;
+        return f;
+      }();
+      const int b0 = block_of(sel, j.kk * PT);
+      const int b1 = PT == 2 ? block_of(sel, j.kk * PT + 1) : b0;
+      const int tt0 = (wave + j.kk * NW) * kTile;
+      if constexpr (F8)
+        load_tile_fp8<D, BS>(t, kbase, vbase, p.k_block_stride, p.v_block_stride, b0, b1, tt0, g, col);
+      else
+        load_tile<D, BS>(t, kbase, vbase, p.k_block_stride, p.v_block_stride, b0, b1, tt0, g, col);
+    };
+    auto consume_job = [&](TileT& t, Job j, WaveAcc<D>& acc) {
+      const int tt0 = (wave + j.kk * NW) * kTile;
+      int t1 = tt0 + kTile;
+#pragma unroll
+      for (int i = 0; i < S; ++i)
+        if (j.i == i) t1 = (int)it.ctx[i];
+      const bool on = lane_live && (j.i < 0 || ci == j.i);
+      if (tt0 + kTile > t1)
+        consume_tile<QT, CT, D, BS, false, true, true>(p, t, tt0, t1, lane_ctx, g, col, qa, qb, slope, acc, on);
+      else
+        consume_tile<QT, CT, D, BS, false, false, true>(p, t, tt0, t1, lane_ctx, g, col, qa, qb, slope, acc, on);
+    };
+
+    WaveAcc<D> acc;
+    acc.init();
+    Job cur = job_at_tile(0);
+    if (cur.kk >= 0) {
+      TileT ta, tb;
+      load_job(ta, cur);
+      while (true) {
+        Job nx = next_job(cur);
+        if (nx.kk >= 0) load_job(tb, nx);
+        __builtin_amdgcn_s_waitcnt(kWaitAhead);
+        consume_job(ta, cur, acc);
+        if (nx.kk < 0) break;
+        cur = nx;
+        nx = next_job(cur);
+        if (nx.kk >= 0) load_job(ta, nx);
+        __builtin_amdgcn_s_waitcnt(kWaitAhead);
+        consume_job(tb, cur, acc);
+        if (nx.kk < 0) break;
+        cur = nx;
+      }
+    }
+    merge_store_waves<QT, D, NW>(p, acc, s_red[buf], s_m[buf], s_l[buf], wave, lane, g, col,
+                                 (int64_t)lane_seq * p.num_heads + it.kvh * grp + hc, col_used && lane_seq >= 0);
+    if (!has_next) break;
+    it = nit;
+#pragma unroll
+    for (int i = 0; i < S; ++i) blk[i] = nblk[i];
 #pragma unroll
     for (int j = 0; j < KSTEPS; ++j) qa[j] = nqa[j];
     if constexpr (SPLIT_Q) {
@@ -1382,10 +1706,46 @@ inline int device_cus() {
 
 // Launches the persistent kernel (BS = 0: token rows) when the batch has
 // enough items for it; *launched says whether it did.
+// The grouped kernel when the batch fills it (at least two items of S
+// sequences per resident workgroup), GQA groups fit S to the 16 columns and
+// contexts fit its register-held block ids.
+template <class QT, class CT, int D, int BS>
+static hipError_t launch_grouped(const DecodeParams& p, hipStream_t stream, bool* launched) {
+  *launched = false;
+  constexpr int S = kGroupSeqs;
+  if (p.slices != 1 || p.group * S > 16 || p.max_seq_len > kGroupMaxSeq) return hipSuccess;
+  constexpr int NT = 64 * Persist<D>::kWaves;
+  static int per_cu = -1;
+  if (per_cu < 0) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, paged_decode_group_kernel<QT, CT, D, BS, S>, NT, 0) !=
+            hipSuccess ||
+        n <= 0)
+      n = 1;
+    per_cu = n;
+  }
+  const int64_t items = (int64_t)((p.num_seqs + S - 1) / S) * p.num_kv_heads;
+  const int64_t grid = (int64_t)device_cus() * per_cu;
+  if (grid <= 0 || items < 2 * grid) return hipSuccess;
+  *launched = true;
+  hipLaunchKernelGGL((paged_decode_group_kernel<QT, CT, D, BS, S>), dim3((unsigned)grid), dim3(NT), 0, stream, p);
+  return hipGetLastError();
+}
+
 template <class QT, class CT, int D, int BS>
 static hipError_t launch_persistent(const DecodeParams& p, hipStream_t stream, bool* launched) {
   *launched = false;
   if (!p.persistent) return hipSuccess;
+  // The grouped kernel's two job buffers leave no register room (it would
+  // spill) above head size 128, for FP8 tiles at 112 and 128 and for a
+  // float32 query with 8-token blocks at 112 and above; those keep the
+  // one-sequence kernel.
+  constexpr bool kGroupable = BS > 0 && D <= 128 && !std::is_same<CT, FP8>::value &&
+                              !(std::is_same<QT, F32>::value && BS == 8 && D >= 112);
+  if constexpr (kGroupable) {
+    const hipError_t ge = launch_grouped<QT, CT, D, BS>(p, stream, launched);
+    if (*launched || ge != hipSuccess) return ge;
+  }
   constexpr int NT = 64 * Persist<D, BS == 0>::kWaves;
   static int per_cu = -1;  // resident workgroups per CU for this instantiation
   if (per_cu < 0) {

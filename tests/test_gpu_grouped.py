@@ -1,0 +1,140 @@
+"""GPU parity of the grouped persistent decode (items of four sequences whose
+query heads share one MFMA; tiles that all four map to the same blocks are
+loaded once) against the oracle.  The launcher picks it when a batch gives
+at least two such items per resident workgroup (here 256 sequences x 8 KV
+heads and up) with GQA groups of at most 4 and contexts up to 8192 tokens.
+Cases: radix-shared prefixes (whole and partially filled last blocks),
+unshared batches, partial groups, empty and over-long contexts, masked
+block ids, ALiBi, MHA and GQA 2, block sizes 8/16/32, fp16 and float32
+queries, and more than 1024 sequences (no longest-first order)."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import pagedkv_oracle as orc
+from pkv_cases import X_OF, normal, tolerance
+from pkv_torch import to_f64, to_index, to_torch
+from sglang_mlx_amd import kernels
+
+pytestmark = pytest.mark.gpu
+
+
+def radix_case(seed, B, Hq, Hkv, D, bs, prefix_tokens, suffix_lo, suffix_hi, dtype="bfloat16", q_dtype=None,
+               share=True, alibi=False):
+    """Every sequence starts with the same prefix blocks (when share), then
+    private blocks; the pool holds random values everywhere."""
+    rng = np.random.default_rng(seed)
+    q_dtype = q_dtype or dtype
+    npb = -(-prefix_tokens // bs)
+    ctx = (prefix_tokens + rng.integers(suffix_lo, suffix_hi + 1, size=B)).astype(np.int32)
+    nblk = -(-ctx // bs)
+    private = nblk - (npb if share else 0)
+    nb = int(private.sum() + npb + 2)
+    perm = rng.permutation(np.arange(1, nb))
+    prefix_ids = perm[:npb]
+    pos = npb
+    width = int(nblk.max())
+    bt = np.full((B, width), -1, dtype=np.int32)
+    for s in range(B):
+        if share:
+            bt[s, :npb] = prefix_ids
+            bt[s, npb:nblk[s]] = perm[pos:pos + private[s]]
+        else:
+            bt[s, :nblk[s]] = perm[pos:pos + private[s]]
+        pos += private[s]
+    x = X_OF[dtype]
+    kc = normal(rng, (nb, Hkv, D // x, bs, x), dtype)
+    vc = normal(rng, (nb, Hkv, D, bs), dtype)
+    q = normal(rng, (B, Hq, D), q_dtype)
+    slopes = rng.uniform(0.01, 0.2, size=Hq).astype(np.float32) if alibi else None
+    return dict(q=q, kc=kc, vc=vc, bt=bt, ctx=ctx, Hkv=Hkv, bs=bs, dt=dtype, qd=q_dtype, alibi=slopes,
+                scale=1.0 / math.sqrt(D))
+
+
+def run(c):
+    alibi = None if c["alibi"] is None else torch.from_numpy(c["alibi"]).cuda()
+    out = kernels.paged_attention_v1(to_torch(c["q"], c["qd"]), to_torch(c["kc"], c["dt"]), to_torch(c["vc"], c["dt"]),
+                                     to_index(c["bt"]), to_index(c["ctx"]), c["Hkv"], c["scale"], c["bs"],
+                                     int(c["bt"].shape[1] * c["bs"]), alibi)
+    torch.cuda.synchronize()
+    return out
+
+
+def oracle(c):
+    return orc.paged_attention(c["q"], c["kc"], c["vc"], c["bt"], c["ctx"], c["Hkv"], c["scale"], c["bs"],
+                               int(c["bt"].shape[1] * c["bs"]), c["alibi"], q_dtype=c["qd"], cache_dtype=c["dt"])
+
+
+def expected_masked(c):
+    """Oracle attention with the kernels' masking of block ids outside
+    [0, num_blocks): such blocks' tokens are left out of the softmax."""
+    kc = orc.decode(c["kc"], c["dt"])
+    vc = orc.decode(c["vc"], c["dt"])
+    nb, H, dx, bs, x = kc.shape
+    q = orc.decode(c["q"], c["qd"])
+    out = np.zeros(q.shape)
+    max_seq_len = c["bt"].shape[1] * bs
+    for s in range(q.shape[0]):
+        ctx = int(c["ctx"][s])
+        if ctx == 0 or ctx > max_seq_len:
+            continue
+        t = np.arange(ctx)
+        b = c["bt"][s, t // bs].astype(np.int64)
+        ok = (b >= 0) & (b < nb)
+        k = kc[b[ok], :, :, (t % bs)[ok], :].reshape(-1, H, dx * x)
+        v = vc[b[ok], :, :, (t % bs)[ok]]
+        bias = None if c["alibi"] is None else orc.alibi_bias(c["alibi"], ctx)[:, ok]
+        out[s] = orc._softmax_attend(q[s], k, v, c["scale"], bias)
+    return out
+
+
+def check(c):
+    a, r = tolerance(c["qd"], c["dt"])
+    np.testing.assert_allclose(to_f64(run(c)), oracle(c), atol=a, rtol=r)
+
+
+@pytest.mark.parametrize("prefix", [256, 250])  # whole blocks / a partly filled last shared block
+def test_radix_shared_prefix(prefix):
+    check(radix_case(6000 + prefix, B=256, Hq=32, Hkv=8, D=128, bs=16, prefix_tokens=prefix, suffix_lo=1,
+                     suffix_hi=200))
+
+
+def test_unshared_batch_and_partial_group():
+    check(radix_case(6100, B=258, Hq=32, Hkv=8, D=128, bs=16, prefix_tokens=0, suffix_lo=1, suffix_hi=400,
+                     share=False))
+
+
+def test_empty_overlong_and_masked():
+    c = radix_case(6200, B=256, Hq=32, Hkv=8, D=64, bs=16, prefix_tokens=128, suffix_lo=1, suffix_hi=100,
+                   dtype="float16")
+    c["ctx"][[3, 77, 200]] = 0
+    c["ctx"][150] = c["bt"].shape[1] * 16 + 5   # past max_seq_len: zero row
+    c["bt"][:, 2] = -1                           # a shared block masked out in every sequence
+    c["bt"][10, 5] = c["kc"].shape[0] + 3        # one sequence's shared block out of the pool
+    out = to_f64(run(c))
+    np.testing.assert_allclose(out, expected_masked(c), atol=2e-3, rtol=1e-2)
+    assert not out[[3, 77, 150, 200]].any()
+
+
+@pytest.mark.parametrize("bs", [8, 32])
+def test_block_sizes_and_alibi(bs):
+    check(radix_case(6300 + bs, B=256, Hq=32, Hkv=8, D=128, bs=bs, prefix_tokens=192, suffix_lo=1, suffix_hi=150,
+                     alibi=True))
+
+
+@pytest.mark.parametrize("Hq,Hkv,B", [(8, 8, 1024), (16, 8, 256)])  # MHA (group 1), GQA 2
+def test_group_sizes(Hq, Hkv, B):
+    check(radix_case(6400 + Hq, B=B, Hq=Hq, Hkv=Hkv, D=64, bs=16, prefix_tokens=64, suffix_lo=1, suffix_hi=60))
+
+
+@pytest.mark.parametrize("q_dtype,dtype", [("float32", "bfloat16"), ("float32", "float16"), ("float16", "float16")])
+def test_query_types(q_dtype, dtype):
+    check(radix_case(6500, B=256, Hq=32, Hkv=8, D=96, bs=16, prefix_tokens=160, suffix_lo=1, suffix_hi=120,
+                     dtype=dtype, q_dtype=q_dtype))
+
+
+def test_more_than_1024_sequences():
+    check(radix_case(6600, B=1100, Hq=8, Hkv=2, D=64, bs=16, prefix_tokens=48, suffix_lo=1, suffix_hi=40))
