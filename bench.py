@@ -145,13 +145,35 @@ def timed_launches(fn, steps: int, warmup: int):
     return wall, a.elapsed_time(b) * 1e-3
 
 
+_SLEEP_CYCLES_PER_US = None
+
+
+def queue_ahead(us: float = 80.0):
+    """Queue about `us` microseconds of GPU spinning (torch.cuda._sleep) so that
+    an event recorded next fires only after the host has also queued the
+    launch that follows it: a single launch's event window then holds the
+    kernel, not the host's argument checks and launch call."""
+    global _SLEEP_CYCLES_PER_US
+    if _SLEEP_CYCLES_PER_US is None:
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        torch.cuda._sleep(1_000_000)
+        b.record()
+        torch.cuda.synchronize()
+        _SLEEP_CYCLES_PER_US = 1_000_000 / max(a.elapsed_time(b) * 1e3, 1.0)
+    torch.cuda._sleep(int(us * _SLEEP_CYCLES_PER_US))
+
+
 def per_launch_ms(fn, launches: int, offset: int = 0):
     """Device time of single launches: a HIP event pair around each of
-    `launches` calls (outside the timed region; the events add gaps)."""
+    `launches` calls, each queued behind a GPU spin (queue_ahead) so that the
+    window holds the kernel alone."""
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(launches)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(launches)]
     torch.cuda.synchronize()
     for i in range(launches):
+        queue_ahead()
         starts[i].record()
         fn(offset + i)
         ends[i].record()
@@ -403,15 +425,16 @@ def bench_splitk(dev, kernels, launches: int = 24):
                 method=f"HIP graph of {launches} calls over rotated pools, median of 5 replays")
 
 
-def bench_radix(dev, kernels, steps: int = 40, warmup: int = 5, layers: int = 2):
+def bench_radix(dev, kernels, steps: int = 40, warmup: int = 5, layers: int = 4):
     """Radix-shared decode: 256 sequences (Llama-3-8B heads: 32 q / 8 kv,
     D128, bs16, bf16) whose block tables all start with the same 128 blocks
     (a 2048-token shared prefix) followed by 64..512 private tokens.  Between
     steps 10% of the private blocks are freed through the block allocator
     (LIFO), re-allocated, their K/V rewritten with the append kernel into the
-    paged caches, and the tables rebuilt.  Each step decodes one of `layers`
-    independent layer pools (each with its own prefix blocks); the decode
-    launch alone is timed with a HIP event pair."""
+    paged caches, and the tables rebuilt.  Each step then decodes every one
+    of `layers` independent layer pools (each with its own prefix blocks)
+    back to back, as a model's layers would run; a HIP event pair around
+    those launches, divided by `layers`, is the step's time per launch."""
     from sglang_mlx_amd.srt.mem_cache import BlockAllocator, BlockTable, build_block_tables
 
     B, Hq, Hkv, D, bs = 256, 32, 8, 128, 16
@@ -459,15 +482,16 @@ def bench_radix(dev, kernels, steps: int = 40, warmup: int = 5, layers: int = 2)
     times = []
     for it in range(warmup + steps):
         bt, ctx = churn()
-        kc, vc = pools[it % layers]
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        queue_ahead()
         a.record()
-        kernels.paged_attention_v1(q, kc, vc, bt, ctx, Hkv, scale, bs, max_blocks * bs)
+        for kc, vc in pools:
+            kernels.paged_attention_v1(q, kc, vc, bt, ctx, Hkv, scale, bs, max_blocks * bs)
         b.record()
         if it >= warmup:
             times.append((a, b))
     torch.cuda.synchronize()
-    us = sorted(a.elapsed_time(b) * 1e3 for a, b in times)
+    us = sorted(a.elapsed_time(b) * 1e3 / layers for a, b in times)
     med = us[len(us) // 2]
     ctx_np = np.array([t.num_tokens for t in tables], dtype=np.int64)
     logical = decode_bytes(ctx_np, B, Hq, Hkv, D, bs)
@@ -478,7 +502,8 @@ def bench_radix(dev, kernels, steps: int = 40, warmup: int = 5, layers: int = 2)
                 unique_gbs=round(unique / (med * 1e-6) / 1e9, 1),
                 unique_frac=round(unique / (med * 1e-6) / 1e9 / PEAK_GBS, 4),
                 effective_gbs=round(logical / (med * 1e-6) / 1e9, 1), kv_pools_rotated=layers,
-                method=f"median of {steps} decode launches, HIP events around each; churn and append outside")
+                method=(f"median over {steps} steps of a HIP event pair around {layers} back-to-back decode launches "
+                        f"(one per layer pool), divided by {layers}; churn and append outside"))
 
 
 def bench_cpu(res, budget_s):

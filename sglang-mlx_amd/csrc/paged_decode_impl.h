@@ -1341,7 +1341,8 @@ __global__ __launch_bounds__(64 * (Persist<D, BS == 0>::kWaves)) void paged_deco
 // Grouped persistent kernel (paged layout): each item is (S sequences of
 // neighbouring rank, KV head), and the 16 MFMA columns hold the GQA query
 // heads of all S sequences (S * group <= 16).  A wavefront walks its tiles
-// w, w+NW, ... of the longest of the S contexts; tile by tile:
+// w, w+NW, ... of the longest of the S contexts (in the order described at
+// Job below); tile by tile:
 //   * shared -- every live sequence of the item maps the tile to the same
 //     block(s) and holds all 16 of its tokens: the tile is loaded once and
 //     feeds all columns (a radix-shared prefix is read once per S sequences);
@@ -1487,11 +1488,17 @@ __global__ __launch_bounds__(64 * Persist<D>::kWaves) void paged_decode_group_ke
     const CS* kbase = static_cast<const CS*>(p.k_cache) + (int64_t)it.kvh * p.k_head_stride;
     const CS* vbase = static_cast<const CS*>(p.v_cache) + (int64_t)it.kvh * p.v_head_stride;
 
-    // Job = (tile index k of this wavefront, sequence slot i, or -1 for a
-    // shared tile); kk < 0 marks the end.  All wave-uniform.
+    // Job = (position n in this wavefront's tile order, its tile index kk,
+    // sequence slot i, or -1 for a shared tile); kk < 0 marks the end.  All
+    // wave-uniform.  The wavefront takes its K tiles from both ends in turn
+    // (0, K-1, 1, K-2, ...): a shared prefix then alternates with private
+    // tails, so L2-served and HBM-served loads overlap instead of every
+    // workgroup reading its prefix first and its tails last.
     struct Job {
-      int kk, i;
+      int n, kk, i;
     };
+    const int K = maxnt > wave ? (maxnt - 1 - wave) / NW + 1 : 0;
+    auto kk_of = [&](int n) { return (n & 1) ? K - 1 - (n >> 1) : (n >> 1); };
     auto block_of = [&](int i, int e) {
       int b = blk[0].get(e);
 #pragma unroll
@@ -1499,9 +1506,10 @@ __global__ __launch_bounds__(64 * Persist<D>::kWaves) void paged_decode_group_ke
         if (i == s2) b = blk[s2].get(e);
       return b;
     };
-    auto job_at_tile = [&](int kk) -> Job {
+    auto job_at = [&](int n) -> Job {
+      if (n >= K) return Job{n, -1, 0};
+      const int kk = kk_of(n);
       const int tile = wave + kk * NW;
-      if (tile >= maxnt) return Job{-1, 0};
       bool shared = (uint32_t)(tile + 1) * kTile <= minctx;
       int first_live = -1, b0 = 0, b1 = 0;
 #pragma unroll
@@ -1516,20 +1524,20 @@ __global__ __launch_bounds__(64 * Persist<D>::kWaves) void paged_decode_group_ke
           shared = shared && c0 == b0 && c1 == b1;
         }
       }
-      if (shared) return Job{kk, -1};
+      if (shared) return Job{n, kk, -1};
 #pragma unroll
       for (int i = 0; i < S; ++i)
-        if (tile < nt[i]) return Job{kk, i};
-      return Job{-1, 0};  // not reached: tile < maxnt
+        if (tile < nt[i]) return Job{n, kk, i};
+      return Job{n, -1, 0};  // not reached: tile < maxnt
     };
     auto next_job = [&](Job j) -> Job {
       if (j.i >= 0) {
         const int tile = wave + j.kk * NW;
 #pragma unroll
         for (int i = 0; i < S; ++i)
-          if (i > j.i && tile < nt[i]) return Job{j.kk, i};
+          if (i > j.i && tile < nt[i]) return Job{j.n, j.kk, i};
       }
-      return job_at_tile(j.kk + 1);
+      return job_at(j.n + 1);
     };
     auto load_job = [&](TileT& t, Job j) {
       const int sel = j.i >= 0 ? j.i : [&] {
@@ -1562,7 +1570,7 @@ __global__ __launch_bounds__(64 * Persist<D>::kWaves) void paged_decode_group_ke
 
     WaveAcc<D> acc;
     acc.init();
-    Job cur = job_at_tile(0);
+    Job cur = job_at(0);
     if (cur.kk >= 0) {
       TileT ta, tb;
       load_job(ta, cur);
