@@ -230,11 +230,12 @@ int pkv_paged_attention(void* out, const void* query, const void* key_cache, con
   // Token rows: the row stride takes the place of the block stride below.
   const int64_t kbs = rows ? k_block_stride / block_size : k_block_stride;
   const int64_t vbs = rows ? v_block_stride / block_size : v_block_stride;
-  // K: 16-byte loads (8-byte for FP8); V: 8-byte loads in the paged layout
-  // (4-byte for FP8), 16-byte loads of token rows.
+  // K: 16-byte loads; V: 8-byte loads in the paged layout, 16-byte loads of
+  // token rows (the same byte alignment for FP8 caches, whose wide tiles
+  // load 16 K codes and 8 V codes per lane).
   const int64_t cb = elem_bytes(cache_dtype);
-  const int64_t k_align = fp8 ? 8 : 16;
-  const int64_t v_align = rows ? 16 : fp8 ? 4 : 8;
+  const int64_t k_align = 16;
+  const int64_t v_align = rows ? 16 : 8;
   if (!aligned16(key_cache) || (kbs * cb) % k_align != 0 || (k_head_stride * cb) % k_align != 0 ||
       (reinterpret_cast<uintptr_t>(value_cache) % v_align) != 0 || (vbs * cb) % v_align != 0 ||
       (v_head_stride * cb) % v_align != 0)

@@ -84,6 +84,21 @@ def test_head_sizes_partition_path(D):
 
 
 @pytest.mark.parametrize("bs", [8, 32])
+@pytest.mark.parametrize("D", [64, 192, 256])
+def test_wide_head_sizes_block_sizes(D, bs):
+    # Head sizes that are multiples of 64 load 16 K codes and 8 V codes per
+    # lane (the query takes the permuted head dims); 8-token blocks take each
+    # lane's block, 32-token blocks a token offset inside the block.
+    check(fp8_case(5150 + D + bs, B=3, Hq=8, Hkv=2, D=D, bs=bs, ctx_lo=1, ctx_hi=600, q_dtype="float16"))
+    check(fp8_case(5160 + D + bs, B=2, Hq=8, Hkv=2, D=D, bs=bs, ctx_lo=300, ctx_hi=900), partition_size=256)
+
+
+@pytest.mark.parametrize("D", [64, 256])
+def test_persistent_wide_head_sizes(D):
+    check(fp8_case(5170 + D, B=64, Hq=16, Hkv=8, D=D, bs=16, ctx_lo=1, ctx_hi=500))
+
+
+@pytest.mark.parametrize("bs", [8, 32])
 def test_gqa7_alibi_split_k(bs):
     c = fp8_case(5200 + bs, B=4, Hq=28, Hkv=4, D=128, bs=bs, ctx_lo=100, ctx_hi=3000, q_dtype="float16",
                  alibi=True)
@@ -101,11 +116,12 @@ def test_llama3_8b_layer():
     check(c)
 
 
-def test_exponent_15_codes():
+@pytest.mark.parametrize("D,bs", [(64, 16), (128, 8), (96, 32)])
+def test_exponent_15_codes(D, bs):
     # +-inf and NaN codes in K and V: rows where the oracle is non-finite are
     # exactly the kernel's non-finite rows (the hardware would read these
     # codes as E4M3FN numbers 256..448 without the fix-up).
-    c = fp8_case(5400, B=8, Hq=8, Hkv=2, D=64, bs=16, ctx_lo=20, ctx_hi=200)
+    c = fp8_case(5400 + D + bs, B=8, Hq=8, Hkv=2, D=D, bs=bs, ctx_lo=20, ctx_hi=200)
     kc, vc, bt = c["kc"], c["vc"], c["bt"]
     kc[bt[0, 0], 0, 1, 3, 5] = 0x78   # +inf in K of sequence 0
     kc[bt[1, 0], 1, 0, 2, 0] = 0xF8   # -inf
