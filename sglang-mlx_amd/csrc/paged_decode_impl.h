@@ -1280,22 +1280,36 @@ template <int D, bool ROWS = false, bool F8 = false> struct Persist {
 // Longest-first rank of the sequences (ties by index) into s_order, when
 // there are at most kPersistMaxOrder of them (returns whether it did).
 // Empty and over-long contexts (zero rows) count as length 0.  Every thread
-// of the workgroup calls it.
+// of the workgroup calls it.  s_ctx (16-byte aligned) is padded with zeros
+// to a multiple of 4 entries, which never count: a padding entry is not
+// longer than any context, and its index is past every real one.  The
+// count then reads four lengths per LDS load (the same address in every
+// lane, a broadcast), several loads in flight; one load at a time made the
+// count ~1 us of the kernel's start at 64 sequences.
 __device__ __forceinline__ bool rank_sequences(const DecodeParams& p, uint32_t* s_ctx, int32_t* s_order, int tid,
                                                int nt) {
   const int B = p.num_seqs;
   if (B > kPersistMaxOrder) return false;
-  for (int s = tid; s < B; s += nt) {
-    const uint32_t c = (uint32_t)p.context_lens[s];
-    s_ctx[s] = c > (uint32_t)p.max_seq_len ? 0u : c;
+  const int B4 = (B + 3) & ~3;  // kPersistMaxOrder is a multiple of 4
+  for (int s = tid; s < B4; s += nt) {
+    uint32_t c = 0;
+    if (s < B) {
+      c = (uint32_t)p.context_lens[s];
+      c = c > (uint32_t)p.max_seq_len ? 0u : c;
+    }
+    s_ctx[s] = c;
   }
   __syncthreads();
   for (int s = tid; s < B; s += nt) {
     const uint32_t c = s_ctx[s];
     int r = 0;
-    for (int s2 = 0; s2 < B; ++s2) {
-      const uint32_t c2 = s_ctx[s2];
-      r += (c2 > c) || (c2 == c && s2 < s);
+#pragma unroll 4
+    for (int s2 = 0; s2 < B4; s2 += 4) {
+      const uint4 w = *reinterpret_cast<const uint4*>(s_ctx + s2);
+      r += (w.x > c) || (w.x == c && s2 < s);
+      r += (w.y > c) || (w.y == c && s2 + 1 < s);
+      r += (w.z > c) || (w.z == c && s2 + 2 < s);
+      r += (w.w > c) || (w.w == c && s2 + 3 < s);
     }
     s_order[r] = s;
   }
@@ -1326,7 +1340,7 @@ __global__ __launch_bounds__(64 * (Persist<D, BS == 0>::kWaves)) void paged_deco
   __shared__ float4 s_red[2][NW][DT][64];
   __shared__ float s_m[2][NW][16];
   __shared__ float s_l[2][NW][16];
-  __shared__ uint32_t s_ctx[kPersistMaxOrder];
+  __shared__ __align__(16) uint32_t s_ctx[kPersistMaxOrder];
   __shared__ int32_t s_order[kPersistMaxOrder];
 
   const int tid = threadIdx.x;
@@ -1362,33 +1376,22 @@ __global__ __launch_bounds__(64 * (Persist<D, BS == 0>::kWaves)) void paged_deco
       blk.load(row, p.num_blocks, nlb_max, 0, 0, wave, NW, lane);
   };
 
-  int k = 0;
-  const int rank = rank_of(0);
-  if (rank >= total) return;
-  PersistItem it = item_at(rank);
-  Blocks blk;
-  load_blocks(it.seq, blk);
-  uint4 qa[KSTEPS];
-  uint4 qb[SPLIT_Q ? KSTEPS : 1];
-  load_query<QT, typename MmaOf<QT, CT>::type, D, WideFp8<CT, D>::value>(p, it.seq, it.h0, it.nh, g, col, qa, qb);
-  float slope = (p.alibi != nullptr && col < it.nh) ? p.alibi[it.h0 + col] * kLog2e : 0.f;
-
+  // Each item's block ids, query and slope are loaded at its start, after
+  // the previous item's merge.  Loading them one item ahead, while the
+  // previous item streamed, measured 1.5 us slower at the Llama-3-8B layer
+  // (114.2 against 112.7 us): the registers they held cost more than the
+  // latency they hid behind the merge barrier.
   int buf = 0;
-  while (true) {
-    // Next item's metadata, loaded now and used after this item.
-    const int nrank = rank_of(k + 1);
-    const bool has_next = nrank < total;
-    PersistItem nit = it;
-    Blocks nblk;
-    uint4 nqa[KSTEPS];
-    uint4 nqb[SPLIT_Q ? KSTEPS : 1];
-    float nslope = 0.f;
-    if (has_next) {
-      nit = item_at(nrank);
-      load_blocks(nit.seq, nblk);
-      load_query<QT, typename MmaOf<QT, CT>::type, D, WideFp8<CT, D>::value>(p, nit.seq, nit.h0, nit.nh, g, col, nqa, nqb);
-      nslope = (p.alibi != nullptr && col < nit.nh) ? p.alibi[nit.h0 + col] * kLog2e : 0.f;
-    }
+  for (int k = 0;; ++k) {
+    const int rank = rank_of(k);
+    if (rank >= total) break;
+    const PersistItem it = item_at(rank);
+    Blocks blk;
+    load_blocks(it.seq, blk);
+    uint4 qa[KSTEPS];
+    uint4 qb[SPLIT_Q ? KSTEPS : 1];
+    load_query<QT, typename MmaOf<QT, CT>::type, D, WideFp8<CT, D>::value>(p, it.seq, it.h0, it.nh, g, col, qa, qb);
+    const float slope = (p.alibi != nullptr && col < it.nh) ? p.alibi[it.h0 + col] * kLog2e : 0.f;
 
     WaveAcc<D> acc;
     acc.init();
@@ -1401,26 +1404,15 @@ __global__ __launch_bounds__(64 * (Persist<D, BS == 0>::kWaves)) void paged_deco
         blk.kr = __builtin_amdgcn_make_buffer_rsrc((void*)kbase, (short)0, (int)p.k_rows_bytes, kBufferRsrcWord3);
         blk.vr = __builtin_amdgcn_make_buffer_rsrc((void*)vbase, (short)0, (int)p.v_rows_bytes, kBufferRsrcWord3);
       }
-      stream_tiles<QT, CT, D, TBS, NW, MAXT, Persist<D, ROWS, std::is_same<CT, FP8>::value>::kMaxBuf, ROWS, Blocks>(p, kbase, vbase, blk, 0, (int)it.ctx, it.ctx, wave, g,
-                                                              col, qa, qb, slope, acc);
+      stream_tiles<QT, CT, D, TBS, NW, MAXT, Persist<D, ROWS, std::is_same<CT, FP8>::value>::kMaxBuf, ROWS, Blocks>(
+          p, kbase, vbase, blk, 0, (int)it.ctx, it.ctx, wave, g, col, qa, qb, slope, acc);
     }
     // Every wavefront reads s_red[buf] right after this item's barrier and
     // before it reaches the next item's; s_red[buf] is written again only
     // after that one, two items later.
     merge_store_waves<QT, D, NW, ROWS>(p, acc, s_red[buf], s_m[buf], s_l[buf], wave, lane, g, col,
                                        (int64_t)it.seq * p.num_heads + it.h0 + col, col < it.nh);
-    if (!has_next) break;
-    it = nit;
-    blk = nblk;
-#pragma unroll
-    for (int j = 0; j < KSTEPS; ++j) qa[j] = nqa[j];
-    if constexpr (SPLIT_Q) {
-#pragma unroll
-      for (int j = 0; j < KSTEPS; ++j) qb[j] = nqb[j];
-    }
-    slope = nslope;
     buf ^= 1;
-    ++k;
   }
 }
 
@@ -1472,7 +1464,7 @@ __global__ __launch_bounds__(64 * Persist<D>::kWaves) void paged_decode_group_ke
   __shared__ float4 s_red[2][NW][DT][64];
   __shared__ float s_m[2][NW][16];
   __shared__ float s_l[2][NW][16];
-  __shared__ uint32_t s_ctx[kPersistMaxOrder];
+  __shared__ __align__(16) uint32_t s_ctx[kPersistMaxOrder];
   __shared__ int32_t s_order[kPersistMaxOrder];
 
   const int tid = threadIdx.x;
@@ -1531,32 +1523,21 @@ __global__ __launch_bounds__(64 * Persist<D>::kWaves) void paged_decode_group_ke
     slope = (p.alibi != nullptr && on) ? p.alibi[head] * kLog2e : 0.f;
   };
 
-  int k = 0;
-  const int rank = rank_of(0);
-  if (rank >= total) return;
-  GroupItem<S> it;
-  item_at(rank, it);
-  Blocks blk[S];
-  load_blocks(it, blk);
-  uint4 qa[KSTEPS];
-  uint4 qb[SPLIT_Q ? KSTEPS : 1];
-  float slope;
-  load_lane_query(it, qa, qb, slope);
-
+  // Each item's block ids, queries and slopes are loaded at its start (as
+  // in the one-sequence persistent kernel, where loading them an item ahead
+  // measured slower).
   int buf = 0;
-  while (true) {
-    const int nrank = rank_of(k + 1);
-    const bool has_next = nrank < total;
-    GroupItem<S> nit = it;
-    Blocks nblk[S];
-    uint4 nqa[KSTEPS];
-    uint4 nqb[SPLIT_Q ? KSTEPS : 1];
-    float nslope = 0.f;
-    if (has_next) {
-      item_at(nrank, nit);
-      load_blocks(nit, nblk);
-      load_lane_query(nit, nqa, nqb, nslope);
-    }
+  for (int k = 0;; ++k) {
+    const int rank = rank_of(k);
+    if (rank >= total) break;
+    GroupItem<S> it;
+    item_at(rank, it);
+    Blocks blk[S];
+    load_blocks(it, blk);
+    uint4 qa[KSTEPS];
+    uint4 qb[SPLIT_Q ? KSTEPS : 1];
+    float slope;
+    load_lane_query(it, qa, qb, slope);
 
     // ---- the item's jobs ----
     int nt[S];  // tiles per sequence (0: not live)
@@ -1678,19 +1659,7 @@ __global__ __launch_bounds__(64 * Persist<D>::kWaves) void paged_decode_group_ke
     }
     merge_store_waves<QT, D, NW>(p, acc, s_red[buf], s_m[buf], s_l[buf], wave, lane, g, col,
                                  (int64_t)lane_seq * p.num_heads + it.kvh * grp + hc, col_used && lane_seq >= 0);
-    if (!has_next) break;
-    it = nit;
-#pragma unroll
-    for (int i = 0; i < S; ++i) blk[i] = nblk[i];
-#pragma unroll
-    for (int j = 0; j < KSTEPS; ++j) qa[j] = nqa[j];
-    if constexpr (SPLIT_Q) {
-#pragma unroll
-      for (int j = 0; j < KSTEPS; ++j) qb[j] = nqb[j];
-    }
-    slope = nslope;
     buf ^= 1;
-    ++k;
   }
 }
 
