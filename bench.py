@@ -29,6 +29,8 @@ Printed: ONE JSON line with the driver's fields plus
                 64..512 private tokens, with 10% private-block churn through
                 the block allocator and the append kernel between steps;
                 bandwidth over unique bytes (prefix once) and logical bytes;
+  radix_shared_fp8  the same over FP8 E4M3 caches (appends quantise with
+                k_scale / v_scale);
   token_rows    the decode layer on token-row caches: MHATokenPool's
                 [rows, Hkv, D] buffer through slot tables (block size 1) and
                 the flash layout [blocks, 16, Hkv, D];
@@ -75,7 +77,7 @@ def parse_args():
     ap.add_argument("--no-radix", action="store_true", help="skip the radix-shared decode measurement")
     ap.add_argument("--no-rows", action="store_true", help="skip the token-row (MHATokenPool) decode measurement")
     ap.add_argument("--no-fp8", action="store_true", help="skip the FP8-cache decode measurement")
-    ap.add_argument("--only", choices=["decode", "append", "copy", "splitk", "radix", "rows", "fp8"],
+    ap.add_argument("--only", choices=["decode", "append", "copy", "splitk", "radix", "radix_fp8", "rows", "fp8"],
                     help="run one leg and print its own short JSON line (for counter collection under "
                          "rocprofv3 --pmc): the decode layer, the token-major append, or a plain 1 GiB device "
                          "copy whose FETCH_SIZE / WRITE_SIZE calibrate the counters")
@@ -425,7 +427,7 @@ def bench_splitk(dev, kernels, launches: int = 24):
                 method=f"HIP graph of {launches} calls over rotated pools, median of 5 replays")
 
 
-def bench_radix(dev, kernels, steps: int = 40, warmup: int = 5, layers: int = 4):
+def bench_radix(dev, kernels, steps: int = 40, warmup: int = 5, layers: int = 4, fp8: bool = False):
     """Radix-shared decode: 256 sequences (Llama-3-8B heads: 32 q / 8 kv,
     D128, bs16, bf16) whose block tables all start with the same 128 blocks
     (a 2048-token shared prefix) followed by 64..512 private tokens.  Between
@@ -434,7 +436,9 @@ def bench_radix(dev, kernels, steps: int = 40, warmup: int = 5, layers: int = 4)
     paged caches, and the tables rebuilt.  Each step then decodes every one
     of `layers` independent layer pools (each with its own prefix blocks)
     back to back, as a model's layers would run; a HIP event pair around
-    those launches, divided by `layers`, is the step's time per launch."""
+    those launches, divided by `layers`, is the step's time per launch.
+    fp8: the caches hold FP8 E4M3 codes (k_scale 0.05, v_scale 0.02), written
+    by the FP8 append and read by the FP8 decode."""
     from sglang_mlx_amd.srt.mem_cache import BlockAllocator, BlockTable, build_block_tables
 
     B, Hq, Hkv, D, bs = 256, 32, 8, 128, 16
@@ -453,8 +457,20 @@ def bench_radix(dev, kernels, steps: int = 40, warmup: int = 5, layers: int = 4)
     max_blocks = max(len(t.blocks) for t in tables) + 1
     g = torch.Generator(device=dev)
     g.manual_seed(1005)
-    pools = [(torch.randn((nb, Hkv, D // 8, bs, 8), generator=g, device=dev).to(torch.bfloat16),
-              torch.randn((nb, Hkv, D, bs), generator=g, device=dev).to(torch.bfloat16)) for _ in range(layers)]
+    k_scale, v_scale = 0.05, 0.02
+    if fp8:
+        pools = []
+        for _ in range(layers):
+            kc = torch.empty((nb, Hkv, D // 16, bs, 16), dtype=torch.uint8, device=dev)
+            vc = torch.empty((nb, Hkv, D, bs), dtype=torch.uint8, device=dev)
+            kernels.convert_fp8(kc, torch.randn(kc.shape, generator=g, device=dev), k_scale)
+            kernels.convert_fp8(vc, torch.randn(vc.shape, generator=g, device=dev), v_scale)
+            pools.append((kc, vc))
+        scales = dict(k_scale=k_scale, v_scale=v_scale)
+    else:
+        pools = [(torch.randn((nb, Hkv, D // 8, bs, 8), generator=g, device=dev).to(torch.bfloat16),
+                  torch.randn((nb, Hkv, D, bs), generator=g, device=dev).to(torch.bfloat16)) for _ in range(layers)]
+        scales = {}
     q = torch.randn((B, Hq, D), generator=g, device=dev).to(torch.bfloat16)
     src_k = torch.randn((B * 32, Hkv, D), generator=g, device=dev).to(torch.bfloat16)
     src_v = torch.randn((B * 32, Hkv, D), generator=g, device=dev).to(torch.bfloat16)
@@ -475,7 +491,7 @@ def bench_radix(dev, kernels, steps: int = 40, warmup: int = 5, layers: int = 4)
         slots = torch.tensor(slots, dtype=torch.int32).to(dev, non_blocking=True)
         n = slots.shape[0]
         for kc, vc in pools:
-            kernels.reshape_and_cache(src_k[:n], src_v[:n], kc, vc, slots)
+            kernels.reshape_and_cache(src_k[:n], src_v[:n], kc, vc, slots, **scales)
         bt, ctx = build_block_tables(tables, max_blocks)
         return torch.from_numpy(bt).to(dev, non_blocking=True), torch.from_numpy(ctx).to(dev, non_blocking=True)
 
@@ -486,7 +502,7 @@ def bench_radix(dev, kernels, steps: int = 40, warmup: int = 5, layers: int = 4)
         queue_ahead()
         a.record()
         for kc, vc in pools:
-            kernels.paged_attention_v1(q, kc, vc, bt, ctx, Hkv, scale, bs, max_blocks * bs)
+            kernels.paged_attention_v1(q, kc, vc, bt, ctx, Hkv, scale, bs, max_blocks * bs, **scales)
         b.record()
         if it >= warmup:
             times.append((a, b))
@@ -494,10 +510,13 @@ def bench_radix(dev, kernels, steps: int = 40, warmup: int = 5, layers: int = 4)
     us = sorted(a.elapsed_time(b) * 1e3 / layers for a, b in times)
     med = us[len(us) // 2]
     ctx_np = np.array([t.num_tokens for t in tables], dtype=np.int64)
-    logical = decode_bytes(ctx_np, B, Hq, Hkv, D, bs)
-    unique = logical - (B - 1) * shared_blocks * bs * Hkv * D * 2 * 2
-    return dict(workload="radix-shared decode: B256, 32 q / 8 kv heads, D128, bs16, bf16, 128 shared blocks "
-                         "(2048 tokens) + U[64,512] private tokens, 10% private-block evict/realloc churn per step",
+    s_kv = 1 if fp8 else 2
+    logical = decode_bytes(ctx_np, B, Hq, Hkv, D, bs, s_kv=s_kv)
+    unique = logical - (B - 1) * shared_blocks * bs * Hkv * D * 2 * s_kv
+    cache = "FP8 E4M3 caches (k_scale 0.05, v_scale 0.02), bf16 query" if fp8 else "bf16"
+    return dict(workload="radix-shared decode: B256, 32 q / 8 kv heads, D128, bs16, " + cache + ", 128 shared "
+                         "blocks (2048 tokens) + U[64,512] private tokens, 10% private-block evict/realloc churn "
+                         "per step",
                 us_per_launch=round(med, 2), unique_bytes_per_launch=int(unique), logical_bytes_per_launch=int(logical),
                 unique_gbs=round(unique / (med * 1e-6) / 1e9, 1),
                 unique_frac=round(unique / (med * 1e-6) / 1e9 / PEAK_GBS, 4),
@@ -543,6 +562,8 @@ def only_leg(args, dev, kernels):
         print(json.dumps(dict(leg="splitk", **bench_splitk(dev, kernels))))
     elif args.only == "radix":
         print(json.dumps(dict(leg="radix", **bench_radix(dev, kernels))))
+    elif args.only == "radix_fp8":
+        print(json.dumps(dict(leg="radix_fp8", **bench_radix(dev, kernels, fp8=True))))
     elif args.only == "rows":
         print(json.dumps(dict(leg="rows", **bench_rows(dev, kernels))))
     elif args.only == "fp8":
@@ -622,6 +643,8 @@ def main():
         line["split_k"] = bench_splitk(dev, kernels)
     if not args.no_radix:
         line["radix_shared"] = bench_radix(dev, kernels)
+        if not args.no_fp8:
+            line["radix_shared_fp8"] = bench_radix(dev, kernels, fp8=True)
     if not args.no_rows:
         line["token_rows"] = bench_rows(dev, kernels)
     if not args.no_fp8:

@@ -1801,11 +1801,10 @@ static hipError_t launch_persistent(const DecodeParams& p, hipStream_t stream, b
   *launched = false;
   if (!p.persistent) return hipSuccess;
   // The grouped kernel's two job buffers leave no register room (it would
-  // spill) above head size 128, for FP8 tiles at 112 and 128 and for a
-  // float32 query with 8-token blocks at 112 and above; those keep the
-  // one-sequence kernel.
-  constexpr bool kGroupable = BS > 0 && D <= 128 && !std::is_same<CT, FP8>::value &&
-                              !(std::is_same<QT, F32>::value && BS == 8 && D >= 112);
+  // spill) above head size 128 and for a float32 query over FP8 8-token
+  // blocks at 128; those keep the one-sequence kernel.
+  constexpr bool kGroupable = BS > 0 && D <= 128 &&
+                              !(std::is_same<QT, F32>::value && std::is_same<CT, FP8>::value && BS == 8 && D == 128);
   if constexpr (kGroupable) {
     const hipError_t ge = launch_grouped<QT, CT, D, BS>(p, stream, launched);
     if (*launched || ge != hipSuccess) return ge;

@@ -6,7 +6,8 @@ heads and up) with GQA groups of at most 4 and contexts up to 8192 tokens.
 Cases: radix-shared prefixes (whole and partially filled last blocks),
 unshared batches, partial groups, empty and over-long contexts, masked
 block ids, ALiBi, MHA and GQA 2, block sizes 8/16/32, fp16 and float32
-queries, and more than 1024 sequences (no longest-first order)."""
+queries (also with 8-token blocks at head size 128), FP8 E4M3 caches with
+k_scale / v_scale, and more than 1024 sequences (no longest-first order)."""
 
 import math
 
@@ -134,6 +135,56 @@ def test_group_sizes(Hq, Hkv, B):
 def test_query_types(q_dtype, dtype):
     check(radix_case(6500, B=256, Hq=32, Hkv=8, D=96, bs=16, prefix_tokens=160, suffix_lo=1, suffix_hi=120,
                      dtype=dtype, q_dtype=q_dtype))
+
+
+@pytest.mark.parametrize("q_dtype,D", [("float32", 128), ("float32", 112), ("bfloat16", 128)])
+def test_float32_query_8_token_blocks(q_dtype, D):
+    check(radix_case(6700 + D, B=256, Hq=32, Hkv=8, D=D, bs=8, prefix_tokens=120, suffix_lo=1, suffix_hi=90,
+                     dtype="bfloat16", q_dtype=q_dtype))
+
+
+FP8 = "fp8_e4m3"
+FP8_TOL = {"bfloat16": (1e-2, 2e-2), "float16": (2e-3, 1e-2), "float32": (2e-3, 1e-2)}
+
+
+def fp8_radix_case(seed, D, bs, q_dtype, prefix_tokens=160, suffix_hi=150, k_scale=0.05, v_scale=0.02):
+    """radix_case's block tables, contexts and queries over FP8 caches that
+    hold codes of N(0, 1.5) keys / k_scale and N(0, 0.5) values / v_scale."""
+    c = radix_case(seed, B=256, Hq=32, Hkv=8, D=D, bs=bs, prefix_tokens=prefix_tokens, suffix_lo=1,
+                   suffix_hi=suffix_hi, dtype="bfloat16", q_dtype=q_dtype)
+    rng = np.random.default_rng(seed + 1)
+    nb = c["kc"].shape[0]
+    kx = (rng.standard_normal((nb, 8, D // 16, bs, 16)) * 1.5).astype(np.float32)
+    vx = (rng.standard_normal((nb, 8, D, bs)) * 0.5).astype(np.float32)
+    c["kc"] = orc.fp8_e4m3_encode(kx / np.float32(k_scale))
+    c["vc"] = orc.fp8_e4m3_encode(vx / np.float32(v_scale))
+    c.update(dt=FP8, ks=k_scale, vs=v_scale)
+    return c
+
+
+def check_fp8(c):
+    out = kernels.paged_attention_v1(to_torch(c["q"], c["qd"]), to_torch(c["kc"], FP8), to_torch(c["vc"], FP8),
+                                     to_index(c["bt"]), to_index(c["ctx"]), c["Hkv"], c["scale"], c["bs"],
+                                     int(c["bt"].shape[1] * c["bs"]), None, k_scale=c["ks"], v_scale=c["vs"])
+    torch.cuda.synchronize()
+    exp = orc.paged_attention(c["q"], c["kc"], c["vc"], c["bt"], c["ctx"], c["Hkv"], c["scale"], c["bs"],
+                              int(c["bt"].shape[1] * c["bs"]), None, q_dtype=c["qd"], cache_dtype=FP8,
+                              k_scale=c["ks"], v_scale=c["vs"])
+    a, r = FP8_TOL[c["qd"]]
+    np.testing.assert_allclose(to_f64(out), exp, atol=a, rtol=r)
+
+
+@pytest.mark.parametrize("bs", [8, 16, 32])
+def test_fp8_radix_shared_prefix(bs):
+    check_fp8(fp8_radix_case(6800 + bs, D=128, bs=bs, q_dtype="bfloat16"))
+
+
+@pytest.mark.parametrize("q_dtype,D,bs", [("float16", 128, 16), ("float32", 112, 8), ("float32", 64, 16),
+                                          ("bfloat16", 96, 16)])
+def test_fp8_query_types_head_sizes(q_dtype, D, bs):
+    # 64 and 128 take the wide FP8 tiles (permuted query dims), 96 and 112
+    # the 8-code k-steps.
+    check_fp8(fp8_radix_case(6900 + D + bs, D=D, bs=bs, q_dtype=q_dtype))
 
 
 def test_more_than_1024_sequences():
