@@ -1284,8 +1284,8 @@ template <int D, bool ROWS = false, bool F8 = false> struct Persist {
 // to a multiple of 4 entries, which never count: a padding entry is not
 // longer than any context, and its index is past every real one.  The
 // count then reads four lengths per LDS load (the same address in every
-// lane, a broadcast), several loads in flight; one load at a time made the
-// count ~1 us of the kernel's start at 64 sequences.
+// lane, a broadcast) with several loads in flight, instead of one dependent
+// load per sequence: B loads per thread at up to 1024 sequences.
 __device__ __forceinline__ bool rank_sequences(const DecodeParams& p, uint32_t* s_ctx, int32_t* s_order, int tid,
                                                int nt) {
   const int B = p.num_seqs;
@@ -1378,9 +1378,10 @@ __global__ __launch_bounds__(64 * (Persist<D, BS == 0>::kWaves)) void paged_deco
 
   // Each item's block ids, query and slope are loaded at its start, after
   // the previous item's merge.  Loading them one item ahead, while the
-  // previous item streamed, measured 1.5 us slower at the Llama-3-8B layer
-  // (114.2 against 112.7 us): the registers they held cost more than the
-  // latency they hid behind the merge barrier.
+  // previous item streamed, measured 7 us slower at the Llama-3-8B layer
+  // (113.4 against 106.3 us in one process): the registers they held (179
+  // VGPRs against 158) cost more than the latency they hid behind the merge
+  // barrier.
   int buf = 0;
   for (int k = 0;; ++k) {
     const int rank = rank_of(k);
