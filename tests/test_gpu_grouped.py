@@ -187,5 +187,23 @@ def test_fp8_query_types_head_sizes(q_dtype, D, bs):
     check_fp8(fp8_radix_case(6900 + D + bs, D=D, bs=bs, q_dtype=q_dtype))
 
 
+def test_fp8_empty_overlong_and_masked():
+    c = fp8_radix_case(7000, D=64, bs=16, q_dtype="float16", prefix_tokens=128, suffix_hi=100)
+    c["ctx"][[3, 77, 200]] = 0
+    c["ctx"][150] = c["bt"].shape[1] * 16 + 5   # past max_seq_len: zero row
+    c["bt"][:, 2] = -1                           # a shared block masked out in every sequence
+    c["bt"][10, 5] = c["kc"].shape[0] + 3        # one sequence's shared block out of the pool
+    out = kernels.paged_attention_v1(to_torch(c["q"], c["qd"]), to_torch(c["kc"], FP8), to_torch(c["vc"], FP8),
+                                     to_index(c["bt"]), to_index(c["ctx"]), c["Hkv"], c["scale"], c["bs"],
+                                     int(c["bt"].shape[1] * c["bs"]), None, k_scale=c["ks"], v_scale=c["vs"])
+    torch.cuda.synchronize()
+    # The masked oracle over the values the codes stand for.
+    ref = dict(c, kc=(orc.fp8_e4m3_decode(c["kc"]) * np.float32(c["ks"])).astype(np.float32),
+               vc=(orc.fp8_e4m3_decode(c["vc"]) * np.float32(c["vs"])).astype(np.float32), dt="float32")
+    got = to_f64(out)
+    np.testing.assert_allclose(got, expected_masked(ref), atol=2e-3, rtol=1e-2)
+    assert not got[[3, 77, 150, 200]].any()
+
+
 def test_more_than_1024_sequences():
     check(radix_case(6600, B=1100, Hq=8, Hkv=2, D=64, bs=16, prefix_tokens=48, suffix_lo=1, suffix_hi=40))
