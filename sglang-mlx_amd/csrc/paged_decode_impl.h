@@ -1686,23 +1686,17 @@ __global__ __launch_bounds__(64 * kMergeWaves) void paged_decode_reduce_kernel(D
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t row = blockIdx.x;  // seq * Hq + head
-  const int seq = (int)(row / p.num_heads);
-  const uint32_t ctx = (uint32_t)p.context_lens[seq];
-  if (ctx == 0 || ctx > (uint32_t)p.max_seq_len) return;
-  const int nparts = ((int)ctx + p.partition - 1) / p.partition;
-  if (nparts == 1) return;
+  const int seq = (int)(blockIdx.x / (uint32_t)p.num_heads);
   const float2* ml = reinterpret_cast<const float2*>(p.ws_ml) + row * p.max_parts;
   const float* po = p.ws_o + row * p.max_parts * D;
-  float mw = -INFINITY, sw = 0.f;
-  float acc[NDL];
-#pragma unroll
-  for (int k = 0; k < NDL; ++k) acc[k] = 0.f;
-  for (int i0 = wave; i0 < nparts; i0 += NW * U) {
-    float2 e[U];
-    float ov[U][NDL];
+  // Partitions i0 + u*NW of step i0, clamped to `lim` (in-range repeats of
+  // i0 that the accumulation skips).
+  float2 e[U];
+  float ov[U][NDL];
+  auto load_step = [&](int i0, int lim) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int i = i0 + u * NW < nparts ? i0 + u * NW : i0;
+      const int i = i0 + u * NW < lim ? i0 + u * NW : i0;
       e[u] = ml[i];
 #pragma unroll
       for (int k = 0; k < NDL; ++k) {
@@ -1710,6 +1704,12 @@ __global__ __launch_bounds__(64 * kMergeWaves) void paged_decode_reduce_kernel(D
         ov[u][k] = (D % 64 == 0 || d < D) ? po[(int64_t)i * D + d] : 0.f;
       }
     }
+  };
+  float mw = -INFINITY, sw = 0.f;
+  float acc[NDL];
+#pragma unroll
+  for (int k = 0; k < NDL; ++k) acc[k] = 0.f;
+  auto accumulate = [&](int i0, int nparts) {
     float gm = -INFINITY;
 #pragma unroll
     for (int u = 0; u < U; ++u)
@@ -1729,6 +1729,35 @@ __global__ __launch_bounds__(64 * kMergeWaves) void paged_decode_reduce_kernel(D
 #pragma unroll
       for (int k = 0; k < NDL; ++k) acc[k] += w * ov[u][k];
     }
+  };
+  // The first step's partials load together with the context length:
+  // bounded by the workspace's max_parts instead of the row's partition
+  // count, and accumulated (masked by that count) before any branch on it,
+  // so that neither waits for the other.  Rows that need no merge (empty,
+  // over-long or single-partition contexts) read and drop them.  A
+  // wavefront past max_parts loads partition 0 (nparts <= max_parts always).
+  const uint32_t ctx = (uint32_t)p.context_lens[seq];
+  load_step(wave < p.max_parts ? wave : 0, p.max_parts);
+  {
+    // The asm needs every first-step value and the context length, so all
+    // of those loads are issued before it (one round trip); without it the
+    // compiler moves the partial loads past the branches on the context.
+    float anchor = 0.f;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      anchor += e[u].x + e[u].y;
+#pragma unroll
+      for (int k = 0; k < NDL; ++k) anchor += ov[u][k];
+    }
+    asm volatile("" ::"v"(anchor), "s"(ctx));
+  }
+  const bool live = ctx != 0 && ctx <= (uint32_t)p.max_seq_len;
+  const int nparts = live ? ((int)ctx + p.partition - 1) / p.partition : 0;
+  accumulate(wave, nparts);
+  if (nparts <= 1) return;
+  for (int i0 = wave + NW * U; i0 < nparts; i0 += NW * U) {
+    load_step(i0, nparts);
+    accumulate(i0, nparts);
   }
 #pragma unroll
   for (int k = 0; k < NDL; ++k) s_acc[wave][lane + 64 * k] = acc[k];
