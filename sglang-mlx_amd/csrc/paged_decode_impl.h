@@ -1724,10 +1724,14 @@ __global__ __launch_bounds__(64 * kMergeWaves) void paged_decode_reduce_kernel(D
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       // A partition whose tokens were all masked has m = -inf and l = 0.
-      const float w = (i0 + u * NW < nparts && e[u].x != -INFINITY) ? e[u].y * exp2f(e[u].x - mw) : 0.f;
+      // Entries past nparts are selected away rather than weighted by 0:
+      // the first step reads them from workspace this call did not write,
+      // which may hold inf or NaN.
+      const bool use = i0 + u * NW < nparts && e[u].x != -INFINITY;
+      const float w = use ? e[u].y * exp2f(e[u].x - mw) : 0.f;
       sw += w;
 #pragma unroll
-      for (int k = 0; k < NDL; ++k) acc[k] += w * ov[u][k];
+      for (int k = 0; k < NDL; ++k) acc[k] += use ? w * ov[u][k] : 0.f;
     }
   };
   // The first step's partials load together with the context length:

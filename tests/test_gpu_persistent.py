@@ -107,3 +107,21 @@ def test_repeated_calls_are_bit_identical():
         assert torch.equal(o, first)
     a, r = tolerance(c.q_dtype, c.cache_dtype)
     np.testing.assert_allclose(to_f64(first), decode_oracle(c), atol=a, rtol=r)
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_split_k_ignores_unwritten_workspace(D):
+    # The merge reads its first step of partials before it knows a row's
+    # partition count; entries a row did not write this call (its context is
+    # shorter than max_seq_len) must not reach the output, even as NaN.
+    from sglang_mlx_amd import _ext
+    c = make_decode_case(3600 + D, B=3, Hq=8, Hkv=2, D=D, block_size=16, ctx_lo=300, ctx_hi=900,
+                         cache_dtype="bfloat16", max_seq_len=4096)
+    run(c, partition_size=256)                 # creates the cached workspace
+    for scratch in list(_ext._ws_cache.values()):
+        scratch.fill_(0xFF)                    # every float32 word a NaN
+    torch.cuda.synchronize()
+    for ps in (256, None):                     # split-K, and v1 (which splits these few rows too)
+        out = run(c, partition_size=ps)
+        a, r = tolerance(c.q_dtype, c.cache_dtype)
+        np.testing.assert_allclose(to_f64(out), decode_oracle(c), atol=a, rtol=r)
