@@ -37,7 +37,8 @@ import torch.nn.functional as F
 
 def host_threads() -> int:
     """Threads the baseline may use: the process's CPU affinity, capped by
-    OMP_NUM_THREADS when that is set (the GPU box sets it to its CPU share)."""
+    OMP_NUM_THREADS when that is set (a shared host may set it to this job's
+    CPU share)."""
     n = len(os.sched_getaffinity(0))
     env = os.environ.get("OMP_NUM_THREADS")
     if env and env.isdigit() and int(env) > 0:
