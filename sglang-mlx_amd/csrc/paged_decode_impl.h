@@ -341,7 +341,8 @@ __device__ __forceinline__ void load_tile_fp8(Tile<D, true>& t, const uint8_t* k
 // Raw FP8 codes -> MFMA operands (MT = BF16 or F16), exactly: the hardware
 // conversion, and for the rare tile holding a code with exponent 15 (which
 // the hardware reads as an E4M3FN number) the reference's inf / NaN.
-template <class MT, int D> __device__ __forceinline__ void dequant_tile(Tile<D, true>& t) {
+// Returns whether the tile holds exponent-15 codes (+-inf or NaN), K or V.
+template <class MT, int D> __device__ __forceinline__ bool dequant_tile(Tile<D, true>& t) {
   constexpr int KSTEPS = Tile<D>::KSTEPS;
   constexpr int DT = Tile<D>::DT;
   if constexpr (D % 64 == 0) {
@@ -372,7 +373,8 @@ template <class MT, int D> __device__ __forceinline__ void dequant_tile(Tile<D, 
   }
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) t.v[dt] = fp8x4_cvt<MT>(t.v8[dt]);
-  if (__any((probe & 0x80808080u) != 0u)) {
+  const bool special = __any((probe & 0x80808080u) != 0u);
+  if (special) {
 #pragma unroll
     for (int j = 0; j < KSTEPS; ++j) {
       const uint2 lo = fp8x4_exact<MT>(t.k8[j].x), hi = fp8x4_exact<MT>(t.k8[j].y);
@@ -381,6 +383,23 @@ template <class MT, int D> __device__ __forceinline__ void dequant_tile(Tile<D, 
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) t.v[dt] = fp8x4_exact<MT>(t.v8[dt]);
   }
+  return special;
+}
+
+// Whether any V element of a 16-bit tile is +-inf or NaN (wave-wide): the
+// exponent fields' running maximum per 16-bit half (v_pk_max_u16) reaches
+// all ones exactly when some element's exponent is all ones.
+typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+template <class MT, int D> __device__ __forceinline__ bool v_nonfinite(const Tile<D, false>& t) {
+  constexpr unsigned short kExp16 = std::is_same<MT, BF16>::value ? 0x7F80 : 0x7C00;
+  constexpr uint32_t kExp = (uint32_t)kExp16 * 0x00010001u;
+  u16x2_t m = {0, 0};
+#pragma unroll
+  for (int dt = 0; dt < Tile<D>::DT; ++dt) {
+    m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2_t, t.v[dt].x & kExp));
+    m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2_t, t.v[dt].y & kExp));
+  }
+  return __any(m.x == kExp16 || m.y == kExp16);
 }
 
 // ---------------------------------------------------------------------------
@@ -714,7 +733,13 @@ __device__ __forceinline__ void consume_tile(const DecodeParams& p, Tile<D, std:
   constexpr bool F8 = std::is_same<CT, FP8>::value;
   using MT = typename MmaOf<QT, CT>::type;
   const int vtok = tt0 + 4 * g;
-  if constexpr (F8) dequant_tile<MT, D>(t);
+  // COLMASK: inactive columns have p = 0, and 0 * inf = NaN; a tile with a
+  // non-finite V element keeps their accumulators out of the PV product.
+  bool v_special = false;
+  if constexpr (F8) {
+    const bool sp = dequant_tile<MT, D>(t);
+    if constexpr (COLMASK) v_special = sp;
+  }
   if constexpr (ROWS) transpose_tile_rows<D>(t, col);
   bool zero_v = false;
   if constexpr (TAIL) {
@@ -796,6 +821,17 @@ __device__ __forceinline__ void consume_tile(const DecodeParams& p, Tile<D, std:
   acc.l_run += (pr[0] + pr[1]) + (pr[2] + pr[3]);
   // ---- O^T += V^T * P^T ----
   const uint2 pp = make_uint2(pack_p<MT>(pr[0], pr[1]), pack_p<MT>(pr[2], pr[3]));
+  if constexpr (COLMASK) {
+    if constexpr (!F8) v_special = v_nonfinite<MT, D>(t);
+    if (v_special) {
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const f32x4 r = Mma<MT>::k16(t.v[dt], pp, acc.o[dt]);
+        acc.o[dt] = col_on ? r : acc.o[dt];
+      }
+      return;
+    }
+  }
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) acc.o[dt] = Mma<MT>::k16(t.v[dt], pp, acc.o[dt]);
 }
@@ -1835,10 +1871,9 @@ static hipError_t launch_persistent(const DecodeParams& p, hipStream_t stream, b
   *launched = false;
   if (!p.persistent) return hipSuccess;
   // The grouped kernel's two job buffers leave no register room (it would
-  // spill) above head size 128 and for a float32 query over FP8 8-token
-  // blocks at 128; those keep the one-sequence kernel.
-  constexpr bool kGroupable = BS > 0 && D <= 128 &&
-                              !(std::is_same<QT, F32>::value && std::is_same<CT, FP8>::value && BS == 8 && D == 128);
+  // spill) above head size 128 and for 8-token blocks at 112 and above;
+  // those keep the one-sequence kernel.
+  constexpr bool kGroupable = BS > 0 && D <= 128 && !(BS == 8 && D >= 112);
   if constexpr (kGroupable) {
     const hipError_t ge = launch_grouped<QT, CT, D, BS>(p, stream, launched);
     if (*launched || ge != hipSuccess) return ge;

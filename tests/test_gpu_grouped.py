@@ -205,5 +205,46 @@ def test_fp8_empty_overlong_and_masked():
     assert not got[[3, 77, 150, 200]].any()
 
 
+def _poison_last_token_v(c, s, code):
+    """V of sequence s's last context token (KV head 0, dim 5) set to `code`
+    (an inf pattern of the cache type)."""
+    t = int(c["ctx"][s]) - 1
+    c["vc"][c["bt"][s, t // c["bs"]], 0, 5, t % c["bs"]] = code
+
+
+def _check_nonfinite(got, exp, a, r):
+    np.testing.assert_array_equal(np.isfinite(got), np.isfinite(exp))
+    fin = np.isfinite(exp)
+    np.testing.assert_allclose(got[fin], exp[fin], atol=a, rtol=r)
+
+
+def test_nonfinite_v_in_one_private_tail():
+    # One sequence's private V holds +inf: its own output turns non-finite
+    # (as the oracle's), while the other sequences of its item, which share
+    # the MFMA columns and get p = 0 for that tile, stay finite and exact.
+    c = radix_case(7100, B=256, Hq=32, Hkv=8, D=64, bs=16, prefix_tokens=96, suffix_lo=20, suffix_hi=80)
+    for s in (5, 130):
+        _poison_last_token_v(c, s, 0x7F80)
+    got = to_f64(run(c))
+    exp = oracle(c)
+    assert not np.isfinite(exp[5]).all() and np.isfinite(np.delete(exp, [5, 130], axis=0)).all()
+    _check_nonfinite(got, exp, *tolerance(c["qd"], c["dt"]))
+
+
+def test_fp8_nonfinite_v_in_one_private_tail():
+    c = fp8_radix_case(7200, D=128, bs=16, q_dtype="bfloat16", prefix_tokens=96, suffix_hi=80)
+    for s in (7, 200):
+        _poison_last_token_v(c, s, 0x78)  # +inf in the reference's E4M3
+    out = kernels.paged_attention_v1(to_torch(c["q"], c["qd"]), to_torch(c["kc"], FP8), to_torch(c["vc"], FP8),
+                                     to_index(c["bt"]), to_index(c["ctx"]), c["Hkv"], c["scale"], c["bs"],
+                                     int(c["bt"].shape[1] * c["bs"]), None, k_scale=c["ks"], v_scale=c["vs"])
+    torch.cuda.synchronize()
+    exp = orc.paged_attention(c["q"], c["kc"], c["vc"], c["bt"], c["ctx"], c["Hkv"], c["scale"], c["bs"],
+                              int(c["bt"].shape[1] * c["bs"]), None, q_dtype=c["qd"], cache_dtype=FP8,
+                              k_scale=c["ks"], v_scale=c["vs"])
+    assert not np.isfinite(exp[7]).all() and np.isfinite(np.delete(exp, [7, 200], axis=0)).all()
+    _check_nonfinite(to_f64(out), exp, *FP8_TOL[c["qd"]])
+
+
 def test_more_than_1024_sequences():
     check(radix_case(6600, B=1100, Hq=8, Hkv=2, D=64, bs=16, prefix_tokens=48, suffix_lo=1, suffix_hi=40))
