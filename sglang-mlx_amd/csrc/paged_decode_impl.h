@@ -1292,9 +1292,9 @@ __global__ __launch_bounds__(64 * kPartWaves) void paged_decode_rows_kernel(Deco
 // whole (sequence, unit) items and produces their output rows without any
 // partial results.  Items are ranked longest context first and dealt in a
 // snake order (round k gives rank k*G + w to workgroup w, reversed on odd
-// rounds), which balances the workgroups' total work.  While a workgroup
-// streams one item it already loads the next item's context length, block
-// ids and query, so consecutive items follow each other without a gap.
+// rounds), which balances the workgroups' total work.  Each item's context
+// length, block ids and query are loaded at its start, after the previous
+// item's merge (the reason is given at the item loop).
 // ---------------------------------------------------------------------------
 #ifndef PKV_ROWS_WAVES
 #define PKV_ROWS_WAVES 8
