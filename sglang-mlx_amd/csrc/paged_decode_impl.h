@@ -944,7 +944,13 @@ __device__ __forceinline__ void stream_tiles(const DecodeParams& p, const typena
     while (true) {
 #pragma unroll
       for (int b = 0; b < NBUF; ++b) {
+        // Raised wave priority while the next tile's loads issue, so a
+        // wavefront with loads to send wins instruction arbitration over
+        // siblings busy with MFMA work: 106.2 against 106.6 us at the
+        // Llama-3-8B layer, same process (the FP8 layer is unchanged).
+        __builtin_amdgcn_s_setprio(1);
         load(t[(b + NBUF - 1) % NBUF], min(tile + (NBUF - 1) * NW, last));
+        __builtin_amdgcn_s_setprio(0);
         __builtin_amdgcn_s_waitcnt(kWaitAhead);
         consume(Full{}, t[b], t0 + tile * kTile);
         tile += NW;
