@@ -171,7 +171,7 @@ constexpr int kBufferRsrcWord3 = 0x00020000;
 // bounds) and are discarded by the caller.  In both cases the number of
 // loads per tile is fixed, so the next tiles' loads stay in flight while the
 // current one is consumed.
-template <int D, int BS>
+template <int D, int BS, int CPOL = 0>
 __device__ __forceinline__ void load_tile(Tile<D>& t, const uint16_t* kbase, const uint16_t* vbase,
                                           int64_t k_block_stride, int64_t v_block_stride, int b0, int b1, int tt0,
                                           int g, int col) {
@@ -195,11 +195,11 @@ __device__ __forceinline__ void load_tile(Tile<D>& t, const uint16_t* kbase, con
 #pragma unroll
     for (int j = 0; j < Tile<D>::KSTEPS; ++j)
       t.k[j] = __builtin_bit_cast(uint4,
-                                  __builtin_amdgcn_raw_buffer_load_b128(kr, ko + j * (4 * BS * 16), off * 16, 0));
+                                  __builtin_amdgcn_raw_buffer_load_b128(kr, ko + j * (4 * BS * 16), off * 16, CPOL));
 #pragma unroll
     for (int dt = 0; dt < Tile<D>::DT; ++dt)
       t.v[dt] = __builtin_bit_cast(uint2,
-                                   __builtin_amdgcn_raw_buffer_load_b64(vr, vo + dt * (16 * BS * 2), off * 2, 0));
+                                   __builtin_amdgcn_raw_buffer_load_b64(vr, vo + dt * (16 * BS * 2), off * 2, CPOL));
   } else {
     constexpr int NCHUNK = D / 8;  // 16-byte K chunks per token
     const int kpb = col < 8 ? b0 : b1;  // K row = token tt0 + col
@@ -242,7 +242,7 @@ __device__ __forceinline__ void load_tile(Tile<D>& t, const uint16_t* kbase, con
 // load instruction covers 32 whole dimension rows.  dequant_tile then swaps
 // rows between the two words (v_permlane16_swap) so that v8[2i] and
 // v8[2i+1] become the operands of dimension tiles 2i and 2i+1.
-template <int D, int BS>
+template <int D, int BS, int CPOL = 0>
 __device__ __forceinline__ void load_tile_fp8(Tile<D, true>& t, const uint8_t* kbase, const uint8_t* vbase,
                                               int64_t k_block_stride, int64_t v_block_stride, int b0, int b1, int tt0,
                                               int g, int col) {
@@ -266,13 +266,13 @@ __device__ __forceinline__ void load_tile_fp8(Tile<D, true>& t, const uint8_t* k
 #pragma unroll
       for (int m = 0; m < KM; ++m) {
         const uint4 w =
-            __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(kr, ko + m * (4 * BS * 16), off * 16, 0));
+            __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(kr, ko + m * (4 * BS * 16), off * 16, CPOL));
         t.k8[2 * m] = make_uint2(w.x, w.y);
         t.k8[2 * m + 1] = make_uint2(w.z, w.w);
       }
 #pragma unroll
       for (int i = 0; i < VI; ++i) {
-        const uint2 w = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(vr, vo + i * (32 * BS), off, 0));
+        const uint2 w = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(vr, vo + i * (32 * BS), off, CPOL));
         t.v8[2 * i] = w.x;
         t.v8[2 * i + 1] = w.y;
       }
@@ -313,12 +313,12 @@ __device__ __forceinline__ void load_tile_fp8(Tile<D, true>& t, const uint8_t* k
       const int c = 4 * j + g;
       t.k8[j] = (NCHUNK % 4 == 0 || c < NCHUNK)
                     ? __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(kr, ko + j * (2 * BS * 16),
-                                                                                      off * 16, 0))
+                                                                                      off * 16, CPOL))
                     : make_uint2(0, 0);
     }
 #pragma unroll
     for (int dt = 0; dt < Tile<D>::DT; ++dt)
-      t.v8[dt] = __builtin_amdgcn_raw_buffer_load_b32(vr, vo + dt * (16 * BS), off, 0);
+      t.v8[dt] = __builtin_amdgcn_raw_buffer_load_b32(vr, vo + dt * (16 * BS), off, CPOL);
   } else {
     const int kpb = col < 8 ? b0 : b1;  // K row = token tt0 + col
     t.kpb = kpb;
@@ -501,7 +501,7 @@ __device__ __forceinline__ void load_tile_rows(Tile<D>& t, const uint16_t* kbase
 // load_tile_rows through buffer resources with 32-bit byte offsets (the
 // persistent kernel's form; k_bytes/v_bytes bound the reachable range):
 // one VGPR per address and no 64-bit arithmetic per tile.
-template <int D>
+template <int D, int CPOL = 0>
 __device__ __forceinline__ void load_tile_rows_buf(Tile<D>& t, __amdgpu_buffer_rsrc_t kr, __amdgpu_buffer_rsrc_t vr,
                                                    uint32_t k_row_bytes, uint32_t v_row_bytes, int rk, int rv, int g,
                                                    int col) {
@@ -520,7 +520,7 @@ __device__ __forceinline__ void load_tile_rows_buf(Tile<D>& t, __amdgpu_buffer_r
   for (int j = 0; j < Tile<D>::KSTEPS; ++j) {
     const int c = 4 * j + g;
     t.k[j] = (NCHUNK % 4 == 0 || c < NCHUNK)
-                 ? __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(kr, ko + j * 64, 0, 0))
+                 ? __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(kr, ko + j * 64, 0, CPOL))
                  : make_uint4(0, 0, 0, 0);
   }
   constexpr int PAIRS = Tile<D>::DT / 2;
@@ -528,7 +528,7 @@ __device__ __forceinline__ void load_tile_rows_buf(Tile<D>& t, __amdgpu_buffer_r
   for (int e = 0; e < PAIRS; ++e) {
     const int d = 32 * e + 8 * (col >> 2);
     const uint4 x = (D % 32 == 0 || d < D)
-                        ? __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(vr, vo + e * 64, 0, 0))
+                        ? __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(vr, vo + e * 64, 0, CPOL))
                         : make_uint4(0, 0, 0, 0);
     t.v[2 * e] = make_uint2(x.x, x.y);
     t.v[2 * e + 1] = make_uint2(x.z, x.w);
@@ -538,7 +538,7 @@ __device__ __forceinline__ void load_tile_rows_buf(Tile<D>& t, __amdgpu_buffer_r
     constexpr int dt = Tile<D>::DT - 1;
     const int d = 16 * dt + 4 * (col >> 2);
     t.v[dt] = d < D ? __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(
-                                                    vr, vo - (uint32_t)(col >> 2) * 8u + dt * 32, 0, 0))
+                                                    vr, vo - (uint32_t)(col >> 2) * 8u + dt * 32, 0, CPOL))
                     : make_uint2(0, 0);
   }
 }
@@ -555,7 +555,7 @@ template <int D> __device__ __forceinline__ void transpose_tile_rows(Tile<D>& t,
 // lane's (K row, V row) for tile `tile`.
 struct LdsRows {
   const int32_t* rows;
-  template <int D>
+  template <int D, int CPOL = 0>
   __device__ __forceinline__ void load_tile(Tile<D>& t, const DecodeParams& p, const uint16_t* kbase,
                                             const uint16_t* vbase, int tile, int /*k*/, int g, int col) const {
     const int32_t* r = rows + tile * kTile;
@@ -597,11 +597,11 @@ template <int MAXT> struct WaveRows {
       v[c] = ok ? (b[c] << shift) + (t & ((1 << shift) - 1)) : -1;
     }
   }
-  template <int D>
+  template <int D, int CPOL = 0>
   __device__ __forceinline__ void load_tile(Tile<D>& t, const DecodeParams& p, const uint16_t* /*kbase*/,
                                             const uint16_t* /*vbase*/, int /*tile*/, int k, int g, int col) const {
     const int2 r = at(k, g, col);
-    load_tile_rows_buf<D>(t, kr, vr, (uint32_t)p.k_block_stride * 2u, (uint32_t)p.v_block_stride * 2u, r.x, r.y, g,
+    load_tile_rows_buf<D, CPOL>(t, kr, vr, (uint32_t)p.k_block_stride * 2u, (uint32_t)p.v_block_stride * 2u, r.x, r.y, g,
                           col);
   }
   // (K row, V row) of the lane for the wavefront's k-th tile (wave-uniform k).
@@ -878,6 +878,14 @@ __device__ __forceinline__ void load_query_lane(const DecodeParams& p, int seq, 
 // the tiles a wavefront keeps in flight (the default policy's depth suits
 // few workgroups per CU; with a full CU of eight streaming wavefronts, two
 // tiles each keep the memory system just as busy).
+// Cache policy of stream_tiles' paged-layout tile loads: nt (non-temporal),
+// as each K/V tile is read once per launch there.  Same-process medians:
+// Llama-3-8B layer 106.7 -> 96.8 us, its FP8 form 60.2 -> 54.1 us.  Token
+// rows keep the default policy (nt: 121.2 -> 148.0 us, as a 256-byte row is
+// read by several instructions and nt drops its lines in between), and so
+// does the grouped kernel, whose shared-prefix tiles are served from L2.
+constexpr int kStreamCpol = 2;
+
 template <class QT, class CT, int D, int BS, int NW, int MAXT, int MAXBUF = 4, bool ROWS = false,
           class Blocks = WaveBlocks<BS, MAXT>>
 __device__ __forceinline__ void stream_tiles(const DecodeParams& p, const typename Elem<CT>::storage* kbase,
@@ -921,10 +929,10 @@ __device__ __forceinline__ void stream_tiles(const DecodeParams& p, const typena
       const int b0 = blk.get(k * PT);
       const int b1 = PT == 2 ? blk.get(k * PT + 1) : b0;
       if constexpr (F8)
-        load_tile_fp8<D, BS>(t, kbase, vbase, p.k_block_stride, p.v_block_stride, b0, b1, t0 + tile * kTile, g,
+        load_tile_fp8<D, BS, kStreamCpol>(t, kbase, vbase, p.k_block_stride, p.v_block_stride, b0, b1, t0 + tile * kTile, g,
                              col);
       else
-        load_tile<D, BS>(t, kbase, vbase, p.k_block_stride, p.v_block_stride, b0, b1, t0 + tile * kTile, g, col);
+        load_tile<D, BS, kStreamCpol>(t, kbase, vbase, p.k_block_stride, p.v_block_stride, b0, b1, t0 + tile * kTile, g, col);
     }
   };
 
