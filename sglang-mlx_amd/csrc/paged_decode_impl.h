@@ -882,8 +882,10 @@ __device__ __forceinline__ void load_query_lane(const DecodeParams& p, int seq, 
 // as each K/V tile is read once per launch there.  Same-process medians:
 // Llama-3-8B layer 106.7 -> 96.8 us, its FP8 form 60.2 -> 54.1 us.  Token
 // rows keep the default policy (nt: 121.2 -> 148.0 us, as a 256-byte row is
-// read by several instructions and nt drops its lines in between), and so
-// does the grouped kernel, whose shared-prefix tiles are served from L2.
+// read by several instructions and nt drops its lines in between).  The
+// grouped kernel chooses per job: nt for a private tile (read once), the
+// default policy for a shared-prefix tile, which the other items of its KV
+// head then read from L2.
 constexpr int kStreamCpol = 2;
 
 template <class QT, class CT, int D, int BS, int NW, int MAXT, int MAXBUF = 4, bool ROWS = false,
@@ -939,8 +941,9 @@ __device__ __forceinline__ void stream_tiles(const DecodeParams& p, const typena
   // Full tiles: NBUF register sets, the loads of the wavefront's tile
   // i + NW*(NBUF-1) issued before tile i is consumed, so each wavefront keeps
   // NBUF - 1 tiles in flight.  Past its last full tile a wavefront re-reads
-  // that tile (in bounds, served by L2) so that every iteration issues the
-  // same loads.  (Driving the loop by the tile index rather than a 0-based
+  // that tile (in bounds) so that every iteration issues the same loads; with
+  // the nt policy its lines need not still be in L2, so each such repeat may
+  // fetch up to one tile from HBM again (NBUF - 1 per wavefront and item).  (Driving the loop by the tile index rather than a 0-based
   // per-wavefront counter keeps the compiler's register allocation of the
   // rotating tile sets tight.)
   if (first < nfull) {

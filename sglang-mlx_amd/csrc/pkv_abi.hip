@@ -138,6 +138,10 @@ int pkv_reshape_and_cache(const void* key, const void* value, void* key_cache, v
     if (head_size % x != 0) return fail(PKV_ERR_INVALID, "head_size must be a multiple of x");
     if (num_slots % block_size != 0) return fail(PKV_ERR_INVALID, "num_slots must be a multiple of block_size");
   }
+  // The FP8 token-major kernel encodes and stores 8 elements per lane step,
+  // so a row must hold whole groups of 8 (and stays 8-byte aligned).
+  if (fp8 && layout == PKV_LAYOUT_TOKEN_MAJOR && row % 8 != 0)
+    return fail(PKV_ERR_UNSUPPORTED, "FP8 token-major caches need num_kv_heads * head_size to be a multiple of 8");
   if (num_tokens == 0) return PKV_OK;
   if (!key || !value || !key_cache || !value_cache || !slot_mapping)
     return fail(PKV_ERR_INVALID, "null buffer");

@@ -162,6 +162,17 @@ def _check_paged_attention(query, key_cache, value_cache, block_tables, context_
             f"Unsupported query/cache dtype pair for paged_attention: {query.dtype}/{key_cache.dtype}")
     if fp8 and (rows or query.shape[2] % 16):
         raise ValueError("FP8 caches are read in the paged layout with head_size a multiple of 16")
+    if not rows:
+        # The kernels take any block and head strides but read each (block,
+        # head) region as one contiguous run; a cache that is not is
+        # rejected rather than silently copied whole on every call.
+        x = key_cache.shape[4]
+        if key_cache.stride()[2:] != (block_size * x, x, 1):
+            raise ValueError("key_cache must be contiguous within each (block, head) region [head_size/x, "
+                             "block_size, x]")
+        if value_cache.stride()[2:] != (block_size, 1):
+            raise ValueError("value_cache must be contiguous within each (block, head) region [head_size, "
+                             "block_size]")
     if rows:
         # Rows must be [Hkv, D]-contiguous, and the rows of a block evenly
         # spaced (block stride = block_size * row stride).
@@ -190,11 +201,6 @@ def _paged_attention(op, query, key_cache, value_cache, block_tables, context_le
     B, Hq, D = query.shape
     if query.stride(2) != 1 or query.stride(1) != D or (query.stride(0) * _ELEM_BYTES[query.dtype]) % 16:
         query = query.contiguous()
-    if layout == _lib.PKV_LAYOUT_PAGED5D:
-        if key_cache.stride()[2:] != (block_size * key_cache.shape[4], key_cache.shape[4], 1):
-            key_cache = key_cache.contiguous()
-        if value_cache.stride()[2:] != (block_size, 1):
-            value_cache = value_cache.contiguous()
     bt = _as_i32(block_tables)
     lens = _as_i32(context_lens)
     alibi = None if alibi_slopes is None else alibi_slopes.to(torch.float32).contiguous()
@@ -285,6 +291,8 @@ def _reshape_and_cache(op, key, value, key_cache, value_cache, slot_mapping, fla
             raise ValueError("token-major caches must have shape [..., num_kv_heads, head_size]")
         num_slots = key_cache.numel() // (H * D) if H * D else 0
         bs = key_cache.shape[1] if key_cache.dim() == 4 else 1
+        if fp8 and (H * D) % 8:
+            raise ValueError("FP8 token-major caches need num_kv_heads * head_size to be a multiple of 8")
     else:
         raise ValueError("key_cache/value_cache must use a paged or token-major layout")
     if not key_cache.is_contiguous() or not value_cache.is_contiguous():
@@ -389,9 +397,18 @@ def copy_blocks(key_caches, value_caches, block_mapping):
 def swap_blocks(src, dst, block_mapping):
     """dst[m[:, 1]] = src[m[:, 0]] block by block (mlx_cache.cpp:348-370,
     copy_blocks.metal:55-70); updates and returns dst.  Between two tensors on
-    one GPU this is the copy kernel; with one side in host memory (the
-    offload use) each block is one asynchronous copy on the current stream.
-    Pairs with out-of-range block ids are skipped."""
+    one GPU this is the copy kernel.  With one side in host memory (the
+    offload use) the blocks travel through one pinned staging buffer in a
+    single copy on the current stream:
+      host -> GPU: the host gathers the source blocks into pinned memory, one
+        asynchronous copy moves them to a device buffer, and the copy kernel
+        scatters them into dst (nothing waits);
+      GPU -> host: the copy kernel gathers the source blocks into a device
+        buffer, one copy moves them into pinned memory, and after the stream
+        has reached it the host scatters them into dst (the call returns
+        with dst updated).
+    Pairs with out-of-range block ids are skipped.  Tensors on two different
+    GPUs are rejected (this path runs one process per GPU)."""
     _tensor(src)
     _tensor(dst)
     if src.dim() == 0 or dst.dim() == 0 or src.shape[0] == 0 or dst.shape[0] == 0:
@@ -407,9 +424,32 @@ def swap_blocks(src, dst, block_mapping):
         return dst
     if src.device.type != "cuda" and dst.device.type != "cuda":
         raise RuntimeError("SwapBlocks is GPU-only")
-    for s_blk, d_blk in mapping.to("cpu", torch.int64).tolist():
-        if 0 <= s_blk < src.shape[0] and 0 <= d_blk < dst.shape[0]:
-            dst[d_blk].copy_(src[s_blk], non_blocking=True)
+    if src.device.type == "cuda" and dst.device.type == "cuda":
+        raise RuntimeError("SwapBlocks between two GPUs is not supported")
+    m = mapping.to("cpu", torch.int64)
+    keep = (m[:, 0] >= 0) & (m[:, 0] < src.shape[0]) & (m[:, 1] >= 0) & (m[:, 1] < dst.shape[0])
+    m = m[keep]
+    n = m.shape[0]
+    if n == 0:
+        return dst
+    block_shape = tuple(src.shape[1:])
+    block_bytes = src.numel() // src.shape[0] * src.element_size()
+    dev = dst.device if dst.device.type == "cuda" else src.device
+    staging = torch.empty((n,) + block_shape, dtype=src.dtype, pin_memory=True)
+    dev_buf = torch.empty((n,) + block_shape, dtype=src.dtype, device=dev)
+    order = torch.arange(n, dtype=torch.int64)
+    if dst.device.type == "cuda":
+        torch.index_select(src, 0, m[:, 0], out=staging)
+        with torch.cuda.device(dev):
+            dev_buf.copy_(staging, non_blocking=True)
+        # Row i of the device buffer -> block m[i, 1] of dst.
+        _copy_planes([dev_buf], [dst], n, dst.shape[0], block_bytes, torch.stack([order, m[:, 1]], 1), dev)
+    else:
+        _copy_planes([src], [dev_buf], src.shape[0], n, block_bytes, torch.stack([m[:, 0], order], 1), dev)
+        with torch.cuda.device(dev):
+            staging.copy_(dev_buf, non_blocking=True)
+            torch.cuda.current_stream(dev).synchronize()
+        dst[m[:, 1]] = staging
     return dst
 
 

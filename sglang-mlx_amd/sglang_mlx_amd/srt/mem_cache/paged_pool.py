@@ -132,13 +132,20 @@ class BlockTable:
         copies: list[tuple[int, int]] = []
         if n == 0:
             return np.zeros(0, dtype=np.int32), copies
-        if self.num_tokens % bs and allocator.refcount(self.blocks[-1]) > 1:
+        cow = bool(self.num_tokens % bs) and allocator.refcount(self.blocks[-1]) > 1
+        need = max(0, -(-(self.num_tokens + n) // bs) - len(self.blocks))
+        # Every block this call needs is checked for before any state
+        # changes, so a MemoryError leaves the table, its pending
+        # copy-on-write and the allocator as they were (a retry after
+        # eviction then still copies the shared block).
+        if need + cow > allocator.available_size:
+            raise MemoryError(f"Cannot allocate {need + cow} blocks: only {allocator.available_size} available")
+        if cow:
             old = self.blocks[-1]
             (new,) = allocator.alloc(1)
             copies.append((old, new))
             self.blocks[-1] = new
             allocator.free([old])
-        need = -(-(self.num_tokens + n) // bs) - len(self.blocks)
         if need > 0:
             self.blocks.extend(allocator.alloc(need))
         t = np.arange(self.num_tokens, self.num_tokens + n, dtype=np.int64)

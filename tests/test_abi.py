@@ -178,6 +178,12 @@ def rac(**kw):
     (dict(cd=_lib.PKV_FP8_E4M3, x=16, k_scale=0.0), 1, "finite and nonzero"),
     (dict(cd=_lib.PKV_FP8_E4M3, x=16, v_scale=float("inf")), 1, "finite and nonzero"),
     (dict(cd=_lib.PKV_FP8_E4M3, x=16), 1, "null buffer"),
+    # FP8 token-major rows are encoded 8 elements at a time: H * D = 12 and
+    # 4 would leave elements unwritten, so they are rejected.
+    (dict(cd=_lib.PKV_FP8_E4M3, kvd=_lib.PKV_F32, layout=_lib.PKV_LAYOUT_TOKEN_MAJOR, H=1, D=12, ks=12, vs=12),
+     2, "multiple of 8"),
+    (dict(cd=_lib.PKV_FP8_E4M3, layout=_lib.PKV_LAYOUT_TOKEN_MAJOR, H=1, D=4, ks=8, vs=8, N=0), 2, "multiple of 8"),
+    (dict(cd=_lib.PKV_FP8_E4M3, layout=_lib.PKV_LAYOUT_TOKEN_MAJOR, H=3, D=8, ks=24, vs=24), 1, "null buffer"),
 ])
 def test_reshape_and_cache_rejections(kw, code, msg):
     st, err = rac(**kw)

@@ -152,3 +152,33 @@ def test_reshape_and_cache_gpu_only():
     with pytest.raises(RuntimeError, match="GPU-only"):
         kernels.reshape_and_cache(**rac_args(key_cache=torch.zeros(64, 2, 64, dtype=torch.bfloat16),
                                              value_cache=torch.zeros(64, 2, 64, dtype=torch.bfloat16)))
+
+
+def test_paged_cache_regions_must_be_contiguous():
+    # A cache whose (block, head) regions are not one contiguous run would
+    # need a whole-cache copy per call; it is rejected instead.
+    kc = torch.zeros(6, 2, 16, 8, 8, dtype=torch.float16).transpose(2, 3)   # [6, 2, 8, 16, 8] view
+    with pytest.raises(ValueError, match="key_cache must be contiguous within each"):
+        kernels.paged_attention_v1(**pa_args(key_cache=kc))
+    vc = torch.zeros(6, 2, 16, 64, dtype=torch.float16).transpose(2, 3)     # [6, 2, 64, 16] view
+    with pytest.raises(ValueError, match="value_cache must be contiguous within each"):
+        kernels.paged_attention_v1(**pa_args(value_cache=vc))
+    # Block and head strides are free: a slice over blocks passes the checks.
+    big_k = torch.zeros(12, 2, 8, 16, 8, dtype=torch.float16)
+    big_v = torch.zeros(12, 2, 64, 16, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="GPU-only"):
+        kernels.paged_attention_v1(**pa_args(key_cache=big_k[::2], value_cache=big_v[::2]))
+
+
+def test_fp8_token_major_append_needs_rows_of_eight():
+    # Rows of num_kv_heads * head_size = 12 elements cannot be encoded in
+    # groups of 8; 16 can (and then only the GPU is missing).
+    key = torch.zeros(3, 1, 12)
+    cache = torch.zeros(8, 1, 12, dtype=torch.uint8)
+    with pytest.raises(ValueError, match="multiple of 8"):
+        kernels.reshape_and_cache(key, key.clone(), cache, cache.clone(), torch.zeros(3, dtype=torch.int32),
+                                  k_scale=1.0, v_scale=1.0)
+    key = torch.zeros(3, 2, 8)
+    cache = torch.zeros(8, 2, 8, dtype=torch.uint8)
+    with pytest.raises(RuntimeError, match="GPU-only"):
+        kernels.reshape_and_cache(key, key.clone(), cache, cache.clone(), torch.zeros(3, dtype=torch.int32))

@@ -1,0 +1,42 @@
+"""Device-attribute entry points (mlx_device.cpp:12-20, bindings.cpp:125-133):
+get_max_shared_memory_per_block_device_attribute and get_device_attribute,
+through the C-ABI, against torch's own view of the device and against the
+LDS the decode kernels allocate."""
+
+import pytest
+import torch
+
+from sglang_mlx_amd import _ext
+
+pytestmark = pytest.mark.gpu
+
+# hipDeviceAttribute_t values of ROCm 7.2 (hip/hip_runtime_api.h).
+HIP_ATTR_MULTIPROCESSOR_COUNT = 63
+HIP_ATTR_MAX_SHARED_MEMORY_PER_BLOCK = 74
+HIP_ATTR_WARP_SIZE = 87
+
+# LDS of the persistent decode kernel at head size 128 with 8 wavefronts:
+# double-buffered float4 merge tiles [2][8][8][64], (max, sum) [2][2][8][16]
+# floats, and the longest-first order (1024 context lengths + 1024 ranks).
+PERSIST_LDS_BYTES = 2 * 8 * 8 * 64 * 16 + 2 * 2 * 8 * 16 * 4 + 1024 * 4 + 1024 * 4
+
+
+def test_max_shared_memory_per_block():
+    lds = _ext.get_max_shared_memory_per_block_device_attribute()
+    assert lds == _ext.get_device_attribute(HIP_ATTR_MAX_SHARED_MEMORY_PER_BLOCK)
+    assert lds == _ext.get_max_shared_memory_per_block_device_attribute(0)
+    assert PERSIST_LDS_BYTES == 141_312
+    assert lds >= PERSIST_LDS_BYTES       # MI355X: 160 KiB per workgroup
+
+
+def test_device_attribute_matches_torch():
+    props = torch.cuda.get_device_properties(0)
+    assert _ext.get_device_attribute(HIP_ATTR_MULTIPROCESSOR_COUNT) == props.multi_processor_count
+    assert _ext.get_device_attribute(HIP_ATTR_WARP_SIZE, 0) == 64
+
+
+def test_bad_device_raises_runtime_error():
+    with pytest.raises(RuntimeError, match="hipDeviceGetAttribute"):
+        _ext.get_device_attribute(HIP_ATTR_MULTIPROCESSOR_COUNT, torch.cuda.device_count() + 3)
+    with pytest.raises(RuntimeError, match="hipDeviceGetAttribute"):
+        _ext.get_max_shared_memory_per_block_device_attribute(torch.cuda.device_count() + 3)

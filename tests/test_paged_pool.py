@@ -101,6 +101,37 @@ def test_copy_on_write_of_shared_partial_block():
     assert copies == [] and f2.blocks[:2] == t2.blocks
 
 
+def test_failed_append_on_forked_table_changes_nothing():
+    # A 5-block pool (ids 1-4): the parent holds [2, 1] (24 tokens, last
+    # block half full), another table holds [3], the fork shares [2, 1], and
+    # block 4 is free.  Appending 20 tokens to the fork needs the
+    # copy-on-write block plus one growth block: the MemoryError must leave
+    # table, refcounts and free stack untouched, and the retry once block 3
+    # is free must still copy the shared block.
+    a = BlockAllocator(5)
+    parent = BlockTable(16)
+    parent.append_slots(24, a)
+    other = BlockTable(16)
+    other.append_slots(1, a)
+    child = parent.fork(a)
+    assert parent.blocks == [2, 1] and other.blocks == [3]
+
+    def state():
+        return list(child.blocks), child.num_tokens, a.available_size, [a.refcount(b) for b in range(5)]
+
+    before = state()
+    with pytest.raises(MemoryError, match="Cannot allocate 2 blocks: only 1 available"):
+        child.append_slots(20, a)
+    assert state() == before
+    other.release(a)                     # free stack (bottom to top): 4, 3
+    slots, copies = child.append_slots(20, a)
+    assert copies == [(1, 3)]            # the shared half-full block is copied
+    assert child.blocks == [2, 3, 4] and parent.blocks == [2, 1]
+    assert a.refcount(1) == 1 and a.refcount(2) == 2 and a.refcount(3) == 1 and a.refcount(4) == 1
+    assert slots.tolist() == [3 * 16 + o for o in range(8, 16)] + [4 * 16 + o for o in range(12)]
+    assert a.available_size == 0
+
+
 def test_release_and_build_block_tables():
     a = BlockAllocator(16)
     t1, t2 = BlockTable(4), BlockTable(4)
