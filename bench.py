@@ -57,6 +57,7 @@ import torch
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "sglang-mlx_amd"))
+sys.path.insert(0, os.path.join(ROOT, "tests"))
 
 METRIC = "paged decode µs/step + HBM GB/s (% peak), bs64 ctx≤4k Llama-3-8B shape"
 PEAK_GBS = 8000.0  # MI355X HBM3E, published peak
@@ -428,95 +429,43 @@ def bench_splitk(dev, kernels, launches: int = 24):
 
 
 def bench_radix(dev, kernels, steps: int = 40, warmup: int = 5, layers: int = 4, fp8: bool = False):
-    """Radix-shared decode: 256 sequences (Llama-3-8B heads: 32 q / 8 kv,
-    D128, bs16, bf16) whose block tables all start with the same 128 blocks
-    (a 2048-token shared prefix) followed by 64..512 private tokens.  Between
-    steps 10% of the private blocks are freed through the block allocator
-    (LIFO), re-allocated, their K/V rewritten with the append kernel into the
-    paged caches, and the tables rebuilt.  Each step then decodes every one
-    of `layers` independent layer pools (each with its own prefix blocks)
-    back to back, as a model's layers would run; a HIP event pair around
-    those launches, divided by `layers`, is the step's time per launch.
-    fp8: the caches hold FP8 E4M3 codes (k_scale 0.05, v_scale 0.02), written
-    by the FP8 append and read by the FP8 decode."""
-    from sglang_mlx_amd.srt.mem_cache import BlockAllocator, BlockTable, build_block_tables
+    """Radix-shared decode (tests/pkv_workloads.py): 256 sequences (Llama-3-8B
+    heads: 32 q / 8 kv, D128, bs16, bf16) whose block tables all start with
+    the same 128 blocks (a 2048-token shared prefix) followed by 64..512
+    private tokens.  Between steps 10% of the private blocks are evicted and
+    re-allocated through the block allocator (freed in a shuffled order, so
+    blocks change hands), their K/V rewritten with the append kernel, and
+    the tables rebuilt.  Each step then decodes every one of `layers`
+    independent layer pools (each with its own prefix blocks) back to back,
+    as a model's layers would run; a HIP event pair around those launches,
+    divided by `layers`, is the step's time per launch.  fp8: the caches
+    hold FP8 E4M3 codes (k_scale 0.05, v_scale 0.02), written by the FP8
+    append and read by the FP8 decode."""
+    from pkv_workloads import B, BS, D, HKV, HQ, SHARED_BLOCKS, RadixSharedWorkload
 
-    B, Hq, Hkv, D, bs = 256, 32, 8, 128, 16
-    shared_blocks = 128
-    rng = np.random.default_rng(1005)
-    priv_tokens = rng.integers(64, 513, size=B)
-    nb = int((shared_blocks + (-(-priv_tokens // bs)).sum()) * 1.2) + 1
-    alloc = BlockAllocator(nb)
-    shared = alloc.alloc(shared_blocks)
-    tables = []
-    for i in range(B):
-        t = BlockTable.from_prefix(alloc, bs, shared)
-        t.append_slots(int(priv_tokens[i]), alloc)
-        tables.append(t)
-    alloc.free(shared)  # the tables hold the prefix from here on
-    max_blocks = max(len(t.blocks) for t in tables) + 1
-    g = torch.Generator(device=dev)
-    g.manual_seed(1005)
-    k_scale, v_scale = 0.05, 0.02
-    if fp8:
-        pools = []
-        for _ in range(layers):
-            kc = torch.empty((nb, Hkv, D // 16, bs, 16), dtype=torch.uint8, device=dev)
-            vc = torch.empty((nb, Hkv, D, bs), dtype=torch.uint8, device=dev)
-            kernels.convert_fp8(kc, torch.randn(kc.shape, generator=g, device=dev), k_scale)
-            kernels.convert_fp8(vc, torch.randn(vc.shape, generator=g, device=dev), v_scale)
-            pools.append((kc, vc))
-        scales = dict(k_scale=k_scale, v_scale=v_scale)
-    else:
-        pools = [(torch.randn((nb, Hkv, D // 8, bs, 8), generator=g, device=dev).to(torch.bfloat16),
-                  torch.randn((nb, Hkv, D, bs), generator=g, device=dev).to(torch.bfloat16)) for _ in range(layers)]
-        scales = {}
-    q = torch.randn((B, Hq, D), generator=g, device=dev).to(torch.bfloat16)
-    src_k = torch.randn((B * 32, Hkv, D), generator=g, device=dev).to(torch.bfloat16)
-    src_v = torch.randn((B * 32, Hkv, D), generator=g, device=dev).to(torch.bfloat16)
-    scale = 1.0 / math.sqrt(D)
-
-    def churn():
-        """Free 10% of the private blocks, re-allocate, rewrite their tokens."""
-        private = [(i, j) for i, t in enumerate(tables) for j in range(shared_blocks, len(t.blocks))]
-        pick = rng.choice(len(private), size=len(private) // 10, replace=False)
-        victims = [private[k] for k in pick]
-        alloc.free([tables[i].blocks[j] for i, j in victims])
-        fresh = alloc.alloc(len(victims))
-        slots = []
-        for (i, j), blk in zip(victims, fresh):
-            tables[i].blocks[j] = blk
-            ntok = min(bs, tables[i].num_tokens - j * bs)
-            slots.extend(blk * bs + o for o in range(ntok))
-        slots = torch.tensor(slots, dtype=torch.int32).to(dev, non_blocking=True)
-        n = slots.shape[0]
-        for kc, vc in pools:
-            kernels.reshape_and_cache(src_k[:n], src_v[:n], kc, vc, slots, **scales)
-        bt, ctx = build_block_tables(tables, max_blocks)
-        return torch.from_numpy(bt).to(dev, non_blocking=True), torch.from_numpy(ctx).to(dev, non_blocking=True)
-
+    w = RadixSharedWorkload(dev, kernels, layers=layers, fp8=fp8)
     times = []
     for it in range(warmup + steps):
-        bt, ctx = churn()
+        info = w.churn()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         queue_ahead()
         a.record()
-        for kc, vc in pools:
-            kernels.paged_attention_v1(q, kc, vc, bt, ctx, Hkv, scale, bs, max_blocks * bs, **scales)
+        for layer in range(layers):
+            w.decode(layer, info["bt_dev"], info["ctx_dev"])
         b.record()
         if it >= warmup:
             times.append((a, b))
     torch.cuda.synchronize()
     us = sorted(a.elapsed_time(b) * 1e3 / layers for a, b in times)
     med = us[len(us) // 2]
-    ctx_np = np.array([t.num_tokens for t in tables], dtype=np.int64)
+    ctx_np = np.array([t.num_tokens for t in w.tables], dtype=np.int64)
     s_kv = 1 if fp8 else 2
-    logical = decode_bytes(ctx_np, B, Hq, Hkv, D, bs, s_kv=s_kv)
-    unique = logical - (B - 1) * shared_blocks * bs * Hkv * D * 2 * s_kv
+    logical = decode_bytes(ctx_np, B, HQ, HKV, D, BS, s_kv=s_kv)
+    unique = logical - (B - 1) * SHARED_BLOCKS * BS * HKV * D * 2 * s_kv
     cache = "FP8 E4M3 caches (k_scale 0.05, v_scale 0.02), bf16 query" if fp8 else "bf16"
     return dict(workload="radix-shared decode: B256, 32 q / 8 kv heads, D128, bs16, " + cache + ", 128 shared "
                          "blocks (2048 tokens) + U[64,512] private tokens, 10% private-block evict/realloc churn "
-                         "per step",
+                         "per step (blocks change hands)",
                 us_per_launch=round(med, 2), unique_bytes_per_launch=int(unique), logical_bytes_per_launch=int(logical),
                 unique_gbs=round(unique / (med * 1e-6) / 1e9, 1),
                 unique_frac=round(unique / (med * 1e-6) / 1e9 / PEAK_GBS, 4),
