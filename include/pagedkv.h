@@ -185,6 +185,38 @@ int pkv_paged_attention(void* out, const void* query, const void* key_cache,
                         float k_scale, float v_scale, void* stream);
 
 /*
+ * Block-table decode attention that allocates nothing and takes no
+ * workspace.  No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Arguments, semantics and results are
+ * those of pkv_paged_attention without its workspace / workspace_bytes.
+ * The partials of the split-K path live in a static device array of
+ * PKV_NOALLOC_SCRATCH_BYTES per GPU, which the library holds from its first
+ * call on that GPU until the process ends; a call whose sizes need more
+ * (pkv_paged_attention_workspace_size) fails with PKV_ERR_UNSUPPORTED
+ * before any HIP call.  The kernels need no initialised scratch and read
+ * only what the same call wrote, so stale contents from an earlier call do
+ * not matter.  Every call on one GPU shares that GPU's array: calls that
+ * overlap in time on one GPU (different streams, or threads) race and give
+ * undefined results; order them on one stream.  The first call on a GPU
+ * looks the array's address up with hipGetSymbolAddress (no allocation).
+ */
+#define PKV_NOALLOC_SCRATCH_BYTES (32u << 20) /* 32 MiB per GPU */
+int pkv_paged_attention_noalloc(void* out, const void* query, const void* key_cache,
+                                const void* value_cache, const int32_t* block_tables,
+                                const int32_t* context_lens,
+                                const float* alibi_slopes, int32_t num_seqs,
+                                int32_t num_heads, int32_t num_kv_heads,
+                                int32_t head_size, int32_t block_size,
+                                int32_t max_num_blocks_per_seq, int32_t max_seq_len,
+                                int64_t num_blocks, float scale, int64_t q_stride,
+                                int64_t k_block_stride, int64_t k_head_stride,
+                                int64_t v_block_stride, int64_t v_head_stride,
+                                int32_t layout, int32_t partition_size,
+                                int32_t q_dtype, int32_t cache_dtype,
+                                float k_scale, float v_scale, void* stream);
+
+/*
  * Whole-block copies between paged caches.  A block is block_bytes
  * contiguous bytes of a plane (a [num_blocks, ...] cache tensor), so every
  * layout and dtype is the same copy.  For each (src, dst) pair of

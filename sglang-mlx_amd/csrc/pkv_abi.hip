@@ -12,6 +12,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 
 namespace {
 
@@ -186,14 +187,49 @@ size_t pkv_paged_attention_workspace_size(int32_t num_seqs, int32_t num_heads, i
   return pkv::decode_workspace_layout(num_seqs, num_heads, head_size, parts).total;
 }
 
-int pkv_paged_attention(void* out, const void* query, const void* key_cache, const void* value_cache,
-                        const int32_t* block_tables, const int32_t* context_lens, const float* alibi_slopes,
-                        int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads, int32_t head_size,
-                        int32_t block_size, int32_t max_num_blocks_per_seq, int32_t max_seq_len,
-                        int64_t num_blocks, float scale, int64_t q_stride, int64_t k_block_stride,
-                        int64_t k_head_stride, int64_t v_block_stride, int64_t v_head_stride, int32_t layout,
-                        int32_t partition_size, void* workspace, size_t workspace_bytes, int32_t q_dtype,
-                        int32_t cache_dtype, float k_scale, float v_scale, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// Static scratch of pkv_paged_attention_noalloc: one copy per device, kept
+// until the process ends.  Host code never names the array itself (on the
+// host its name is a stand-in, not a device address); it uses the address
+// hipGetSymbolAddress returns for the current device.
+static __device__ __align__(256) unsigned char scratch[PKV_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of the current device's scratch, looked up once per device
+// with that device current.
+int static_scratch(void** ptr) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(PKV_ERR_UNSUPPORTED, "device id beyond the scratch table");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (p == nullptr) return fail(PKV_ERR_HIP, "hipGetSymbolAddress(scratch) returned null");
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return PKV_OK;
+}
+
+// pkv_paged_attention, and with use_scratch the no-allocation variant (the
+// workspace is then the static scratch, fetched after every argument check).
+int paged_attention_impl(void* out, const void* query, const void* key_cache, const void* value_cache,
+                         const int32_t* block_tables, const int32_t* context_lens, const float* alibi_slopes,
+                         int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads, int32_t head_size,
+                         int32_t block_size, int32_t max_num_blocks_per_seq, int32_t max_seq_len,
+                         int64_t num_blocks, float scale, int64_t q_stride, int64_t k_block_stride,
+                         int64_t k_head_stride, int64_t v_block_stride, int64_t v_head_stride, int32_t layout,
+                         int32_t partition_size, void* workspace, size_t workspace_bytes, bool use_scratch,
+                         int32_t q_dtype, int32_t cache_dtype, float k_scale, float v_scale, void* stream) {
   if (num_seqs < 0) return fail(PKV_ERR_INVALID, "num_seqs must be non-negative");
   int32_t ps = 0, parts = 0;
   const int st = resolve_partition(num_seqs, num_heads, num_kv_heads, max_seq_len, block_size, partition_size,
@@ -245,6 +281,15 @@ int pkv_paged_attention(void* out, const void* query, const void* key_cache, con
       (v_head_stride * cb) % v_align != 0)
     return fail(PKV_ERR_INVALID, "cache base or strides are not aligned for vector loads");
   const pkv::DecodeWorkspace w = pkv::decode_workspace_layout(num_seqs, num_heads, head_size, parts);
+  if (use_scratch) {
+    if (w.total > (size_t)PKV_NOALLOC_SCRATCH_BYTES)
+      return fail(PKV_ERR_UNSUPPORTED, "pkv_paged_attention_noalloc needs " + std::to_string(w.total) +
+                                           " bytes of workspace for these sizes, more than its static scratch of " +
+                                           std::to_string((size_t)PKV_NOALLOC_SCRATCH_BYTES) + " bytes");
+    const int sst = static_scratch(&workspace);
+    if (sst != PKV_OK) return sst;
+    workspace_bytes = PKV_NOALLOC_SCRATCH_BYTES;
+  }
   if (workspace == nullptr || workspace_bytes < w.total)
     return fail(PKV_ERR_INVALID, "workspace is smaller than pkv_paged_attention_workspace_size()");
   if (!aligned16(workspace)) return fail(PKV_ERR_INVALID, "workspace must be 16-byte aligned");
@@ -316,6 +361,41 @@ int pkv_paged_attention(void* out, const void* query, const void* key_cache, con
   if (!ok) return fail(PKV_ERR_UNSUPPORTED, "Unsupported head_size/block_size for paged_attention");
   if (e != hipSuccess) return hip_fail(e, "paged_attention launch");
   return PKV_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int pkv_paged_attention(void* out, const void* query, const void* key_cache, const void* value_cache,
+                        const int32_t* block_tables, const int32_t* context_lens, const float* alibi_slopes,
+                        int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads, int32_t head_size,
+                        int32_t block_size, int32_t max_num_blocks_per_seq, int32_t max_seq_len,
+                        int64_t num_blocks, float scale, int64_t q_stride, int64_t k_block_stride,
+                        int64_t k_head_stride, int64_t v_block_stride, int64_t v_head_stride, int32_t layout,
+                        int32_t partition_size, void* workspace, size_t workspace_bytes, int32_t q_dtype,
+                        int32_t cache_dtype, float k_scale, float v_scale, void* stream) {
+  return paged_attention_impl(out, query, key_cache, value_cache, block_tables, context_lens, alibi_slopes, num_seqs,
+                              num_heads, num_kv_heads, head_size, block_size, max_num_blocks_per_seq, max_seq_len,
+                              num_blocks, scale, q_stride, k_block_stride, k_head_stride, v_block_stride,
+                              v_head_stride, layout, partition_size, workspace, workspace_bytes, false, q_dtype,
+                              cache_dtype, k_scale, v_scale, stream);
+}
+
+int pkv_paged_attention_noalloc(void* out, const void* query, const void* key_cache, const void* value_cache,
+                                const int32_t* block_tables, const int32_t* context_lens,
+                                const float* alibi_slopes, int32_t num_seqs, int32_t num_heads,
+                                int32_t num_kv_heads, int32_t head_size, int32_t block_size,
+                                int32_t max_num_blocks_per_seq, int32_t max_seq_len, int64_t num_blocks,
+                                float scale, int64_t q_stride, int64_t k_block_stride, int64_t k_head_stride,
+                                int64_t v_block_stride, int64_t v_head_stride, int32_t layout,
+                                int32_t partition_size, int32_t q_dtype, int32_t cache_dtype, float k_scale,
+                                float v_scale, void* stream) {
+  return paged_attention_impl(out, query, key_cache, value_cache, block_tables, context_lens, alibi_slopes, num_seqs,
+                              num_heads, num_kv_heads, head_size, block_size, max_num_blocks_per_seq, max_seq_len,
+                              num_blocks, scale, q_stride, k_block_stride, k_head_stride, v_block_stride,
+                              v_head_stride, layout, partition_size, nullptr, 0, true, q_dtype, cache_dtype,
+                              k_scale, v_scale, stream);
 }
 
 int pkv_max_shared_memory_per_block(int32_t device_id, int64_t* out) {

@@ -21,6 +21,7 @@ PKV_ERR_HIP = 3
 
 PKV_F32, PKV_F16, PKV_BF16, PKV_FP8_E4M3 = 0, 1, 2, 3
 PKV_LAYOUT_PAGED5D, PKV_LAYOUT_TOKEN_MAJOR = 0, 1
+PKV_NOALLOC_SCRATCH_BYTES = 32 << 20  # static scratch of pkv_paged_attention_noalloc, per GPU
 
 _c_void_p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -51,6 +52,17 @@ SIGNATURES = {
         _i64, _i64, _i64, _i64,                                   # k/v block & head strides
         _i32, _i32,                                               # layout, partition_size
         _c_void_p, _size,                                         # workspace, bytes
+        _i32, _i32,                                               # q dtype, cache dtype
+        _f32, _f32, _c_void_p,                                    # k_scale, v_scale (FP8), stream
+    ]),
+    "pkv_paged_attention_noalloc": (ctypes.c_int, [
+        _c_void_p, _c_void_p, _c_void_p, _c_void_p,              # out, q, kc, vc
+        _c_void_p, _c_void_p, _c_void_p,                          # block_tables, ctx, alibi
+        _i32, _i32, _i32, _i32, _i32,                             # B, Hq, Hkv, D, bs
+        _i32, _i32, _i64,                                         # max_blocks, max_seq_len, nb
+        _f32, _i64,                                               # scale, q_stride
+        _i64, _i64, _i64, _i64,                                   # k/v block & head strides
+        _i32, _i32,                                               # layout, partition_size
         _i32, _i32,                                               # q dtype, cache dtype
         _f32, _f32, _c_void_p,                                    # k_scale, v_scale (FP8), stream
     ]),

@@ -43,15 +43,21 @@ def test_every_declared_symbol_is_exported_with_matching_arity():
         assert len(_lib.SIGNATURES[name][1]) == nparams, name
 
 
-def attn(**kw):
-    """pkv_paged_attention with null buffers and valid defaults, overridden by kw."""
+def attn(noalloc=False, **kw):
+    """pkv_paged_attention (or, with noalloc, pkv_paged_attention_noalloc,
+    which takes no workspace arguments) with null buffers and valid
+    defaults, overridden by kw."""
     a = dict(out=None, q=None, kc=None, vc=None, bt=None, ctx=None, alibi=None, B=2, Hq=8, Hkv=2, D=128, bs=16,
              max_blocks=4, max_seq_len=64, nb=10, scale=1.0, q_stride=1024, kbs=2 * 128 * 16, khs=128 * 16,
              vbs=2 * 128 * 16, vhs=128 * 16, layout=_lib.PKV_LAYOUT_PAGED5D, ps=0, ws=None, ws_bytes=0,
              qd=_lib.PKV_BF16, cd=_lib.PKV_BF16, k_scale=1.0, v_scale=1.0, stream=None)
     a.update(kw)
     lib = _lib.lib()
-    st = lib.pkv_paged_attention(*a.values())
+    if noalloc:
+        del a["ws"], a["ws_bytes"]
+        st = lib.pkv_paged_attention_noalloc(*a.values())
+    else:
+        st = lib.pkv_paged_attention(*a.values())
     return st, lib.pkv_last_error().decode()
 
 
@@ -79,6 +85,24 @@ def attn(**kw):
 def test_paged_attention_rejections(kw, code, msg):
     st, err = attn(**kw)
     assert st == code and msg in err, (st, err)
+    # The no-allocation entry point runs the same checks in the same order.
+    st, err = attn(noalloc=True, **kw)
+    assert st == code and msg in err, (st, err)
+
+
+def test_noalloc_refuses_oversize_before_any_hip_call():
+    # 8 sequences x 32 heads at 64K tokens in 16-token partitions need 545 MB
+    # of partials, more than the 32 MiB static scratch: refused by the
+    # argument checks, so this runs without a GPU.
+    import numpy as np
+    buf = np.zeros(64, dtype=np.uint8)
+    p = ctypes.c_void_p((buf.ctypes.data + 15) // 16 * 16)
+    kw = dict(out=p, q=p, kc=p, vc=p, bt=p, ctx=p, B=8, Hq=32, Hkv=8, max_blocks=4096, max_seq_len=65536,
+              q_stride=32 * 128, kbs=8 * 128 * 16, vbs=8 * 128 * 16, ps=16)
+    assert _lib.lib().pkv_paged_attention_workspace_size(8, 32, 8, 128, 65536, 16) > _lib.PKV_NOALLOC_SCRATCH_BYTES
+    st, err = attn(noalloc=True, **kw)
+    assert st == _lib.PKV_ERR_UNSUPPORTED and "static scratch" in err, (st, err)
+    assert attn(noalloc=True, B=0)[0] == _lib.PKV_OK
 
 
 def test_paged_attention_rejects_misaligned_output():
