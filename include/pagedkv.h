@@ -11,7 +11,10 @@
  *   - Return value: PKV_OK (0) on success, otherwise a PKV_ERR_* code; the
  *     message of the last failure on the calling thread is returned by
  *     pkv_last_error().  Argument checks run before any HIP call, so a
- *     rejected call has no side effect.
+ *     rejected call has no side effect.  A HIP error status describes this
+ *     call only: an error left pending on the thread by earlier HIP calls of
+ *     other code is cleared before launching, and a HIP call of the library
+ *     that fails leaves no pending error behind.
  *   - Launches are asynchronous on `stream` (a hipStream_t passed as void*;
  *     NULL = the legacy default stream).  Nothing synchronises.
  *   - The library allocates no device memory.  Output buffers and the
@@ -159,7 +162,9 @@ size_t pkv_paged_attention_workspace_size(int32_t num_seqs, int32_t num_heads,
  *               (The reference decodes the paged layout only; this is the
  *               gather-free path its pool asks for, memory_pool.py:110-112.)
  * (q_dtype, cache_dtype): (BF16,BF16), (F16,F16), (F32,BF16), (F32,F16),
- *   and (BF16|F16|F32, FP8_E4M3): FP8 caches in the paged layout (x = 16,
+ *   (F32,F32) in the paged layout (x = 4; scores and PV on float32 MFMA, so
+ *   nothing is rounded to 16 bits; the V base and strides then need 16-byte
+ *   alignment), and (BF16|F16|F32, FP8_E4M3): FP8 caches in the paged layout (x = 16,
  *   head_size a multiple of 16) hold codes of K / k_scale and V / v_scale
  *   (pkv_reshape_and_cache); attention runs on decode(code) * scale, i.e.
  *   scores scale * k_scale * (q . decode(k)) and output v_scale *

@@ -338,6 +338,103 @@ __device__ __forceinline__ void load_tile_fp8(Tile<D, true>& t, const uint8_t* k
   }
 }
 
+// ---------------------------------------------------------------------------
+// Float32 caches (the reference's (float, float) instantiation,
+// paged_attention_inst.metal:69): K [D/4][bs][4] and V [D][bs] floats per
+// (block, head).  Scores and PV run on v_mfma_f32_16x16x4_f32 over the
+// values as stored, so K, V, the query and the softmax weights are never
+// rounded to 16 bits.
+//   K: lane (g, col) loads 16-byte chunk 4m + g of token col (dims 16m + 4g
+//      .. +3) into k[m]; score MFMA (m, s) takes component s, so its k-index
+//      g stands for dim 16m + 4g + s, and the query operand carries the same
+//      dim (load_query).
+//   V: lane (g, col) loads tokens 4g .. 4g+3 of dim 16dt + col (16
+//      contiguous bytes of [D][bs]) into v[dt]; PV MFMA r takes component r,
+//      whose k-index g stands for token 4g + r -- the token whose weight for
+//      head col is register r of the score MFMA's output in that lane.
+// ---------------------------------------------------------------------------
+template <int D> struct TileF32 {
+  static constexpr int KM = (D + 15) / 16;  // 16-byte K loads per lane
+  static constexpr int DT = (D + 15) / 16;  // 16-dim tiles of the output (and V loads)
+  float4 k[KM];
+  float4 v[DT];
+  int kpb, vpb;  // as Tile
+};
+
+// The register tile of a cache type, and its load instructions per lane.
+template <class CT, int D> struct TileSel {
+  using type = Tile<D, std::is_same<CT, FP8>::value>;
+  static constexpr int kLoads = Tile<D>::KSTEPS + Tile<D>::DT;
+};
+template <int D> struct TileSel<F32, D> {
+  using type = TileF32<D>;
+  static constexpr int kLoads = TileF32<D>::KM + TileF32<D>::DT;
+};
+template <class CT, int D> using TileOf = typename TileSel<CT, D>::type;
+
+// load_tile for float32 caches; same addressing schemes (buffer resources
+// and a wave-uniform token offset for blocks of 16 and more; per-lane
+// addresses, masked blocks reading block 0, for 8).  Chunks and dims past
+// the head size (D = 120) read as zero.
+template <int D, int BS, int CPOL = 0>
+__device__ __forceinline__ void load_tile_f32(TileF32<D>& t, const float* kbase, const float* vbase,
+                                              int64_t k_block_stride, int64_t v_block_stride, int b0, int b1, int tt0,
+                                              int g, int col) {
+  constexpr int KM = TileF32<D>::KM;
+  constexpr int DT = TileF32<D>::DT;
+  constexpr int NCHUNK = D / 4;  // 16-byte K chunks per token
+  if constexpr (BS >= kTile) {
+    const int b = b0;
+    t.kpb = t.vpb = b;
+    const int off = tt0 % BS;
+    const int64_t bb = b < 0 ? 0 : b;
+    const int bytes = b < 0 ? 0 : D * BS * 4;
+    const __amdgpu_buffer_rsrc_t kr =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(kbase + bb * k_block_stride), (short)0, bytes, kBufferRsrcWord3);
+    const __amdgpu_buffer_rsrc_t vr =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(vbase + bb * v_block_stride), (short)0, bytes, kBufferRsrcWord3);
+    // K chunk c of token u at (c * BS + u) * 16 bytes; V dim d, token u at
+    // (d * BS + u) * 4 bytes.
+    const int ko = (g * BS + col) * 16;
+    const int vo = (col * BS + 4 * g) * 4;
+#pragma unroll
+    for (int m = 0; m < KM; ++m) {
+      const int c = 4 * m + g;
+      t.k[m] = (D % 16 == 0 || c < NCHUNK)
+                   ? __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(kr, ko + m * (4 * BS * 16),
+                                                                                      off * 16, CPOL))
+                   : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const int d = 16 * dt + col;
+      t.v[dt] = (D % 16 == 0 || d < D)
+                    ? __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(vr, vo + dt * (16 * BS * 4),
+                                                                                       off * 4, CPOL))
+                    : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  } else {
+    const int kpb = col < 8 ? b0 : b1;  // K row = token tt0 + col
+    t.kpb = kpb;
+    const float* kp = kbase + (int64_t)(kpb < 0 ? 0 : kpb) * k_block_stride + (col % BS) * 4;
+    const int vpb = g < 2 ? b0 : b1;  // V tokens tt0 + 4g .. +3
+    t.vpb = vpb;
+    const float* vp = vbase + (int64_t)(vpb < 0 ? 0 : vpb) * v_block_stride + ((4 * g) % BS);
+#pragma unroll
+    for (int m = 0; m < KM; ++m) {
+      const int c = 4 * m + g;
+      t.k[m] = (D % 16 == 0 || c < NCHUNK) ? *reinterpret_cast<const float4*>(kp + c * (BS * 4))
+                                           : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const int d = 16 * dt + col;
+      t.v[dt] = (D % 16 == 0 || d < D) ? *reinterpret_cast<const float4*>(vp + d * BS)
+                                       : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+}
+
 // Raw FP8 codes -> MFMA operands (MT = BF16 or F16), exactly: the hardware
 // conversion, and for the rare tile holding a code with exponent 15 (which
 // the hardware reads as an E4M3FN number) the reference's inf / NaN.
@@ -678,6 +775,31 @@ template <int D> struct WaveAcc {
 // Query rows h0 .. h0+nh-1 of sequence seq -> B-operand registers (head =
 // col, dims kstep_dim0(j, g) .. +8); a float32 query is split into hi + lo
 // words.
+// Float32 caches: the float32 query as loaded, dims 16m + 4g .. +3 (the
+// lane's K chunk of TileF32) in word m of (qa, qb): m < KSTEPS in qa, the
+// rest in qb (2 * KSTEPS >= KM for every head size).
+template <int D>
+__device__ __forceinline__ float4 query_f32(const uint4 (&qa)[Tile<D>::KSTEPS], const uint4 (&qb)[Tile<D>::KSTEPS],
+                                            int m) {
+  return __builtin_bit_cast(float4, m < Tile<D>::KSTEPS ? qa[m] : qb[m - Tile<D>::KSTEPS]);
+}
+template <int D>
+__device__ __forceinline__ void load_query_f32(const float* qrow, bool active, int g, uint4 (&qa)[Tile<D>::KSTEPS],
+                                               uint4 (&qb)[Tile<D>::KSTEPS]) {
+  constexpr int KS = Tile<D>::KSTEPS;
+  static_assert(2 * KS >= TileF32<D>::KM, "the float32 query must fit the operand words");
+#pragma unroll
+  for (int m = 0; m < 2 * KS; ++m) {
+    const int d0 = 16 * m + 4 * g;
+    const uint4 w = (active && m < TileF32<D>::KM && d0 < D) ? *reinterpret_cast<const uint4*>(qrow + d0)
+                                                            : make_uint4(0, 0, 0, 0);
+    if (m < KS)
+      qa[m] = w;
+    else
+      qb[m - KS] = w;
+  }
+}
+
 template <class QT, class CT, int D, bool WIDE = false>
 __device__ __forceinline__ void load_query(const DecodeParams& p, int seq, int h0, int nh, int g, int col,
                                            uint4 (&qa)[Tile<D>::KSTEPS],
@@ -685,31 +807,36 @@ __device__ __forceinline__ void load_query(const DecodeParams& p, int seq, int h
   using QS = typename Elem<QT>::storage;
   constexpr bool SPLIT_Q = std::is_same<QT, F32>::value;
   const QS* qrow = static_cast<const QS*>(p.q) + (int64_t)seq * p.q_stride + (int64_t)(h0 + col) * D;
+  if constexpr (std::is_same<CT, F32>::value) {
+    static_assert(SPLIT_Q, "float32 caches take a float32 query");
+    load_query_f32<D>(qrow, col < nh, g, qa, qb);
+  } else {
 #pragma unroll
-  for (int j = 0; j < Tile<D>::KSTEPS; ++j) {
-    const int d0 = kstep_dim0<WIDE>(j, g);
-    uint4 a = make_uint4(0, 0, 0, 0), b = make_uint4(0, 0, 0, 0);
-    if (col < nh && d0 < D) {
-      if constexpr (SPLIT_Q) {
-        const float4 x0 = *reinterpret_cast<const float4*>(qrow + d0);
-        const float4 x1 = *reinterpret_cast<const float4*>(qrow + d0 + 4);
-        uint32_t h[8], l[8];
-        split_q<CT>(x0.x, h[0], l[0]);
-        split_q<CT>(x0.y, h[1], l[1]);
-        split_q<CT>(x0.z, h[2], l[2]);
-        split_q<CT>(x0.w, h[3], l[3]);
-        split_q<CT>(x1.x, h[4], l[4]);
-        split_q<CT>(x1.y, h[5], l[5]);
-        split_q<CT>(x1.z, h[6], l[6]);
-        split_q<CT>(x1.w, h[7], l[7]);
-        a = make_uint4(pack2(h[0], h[1]), pack2(h[2], h[3]), pack2(h[4], h[5]), pack2(h[6], h[7]));
-        b = make_uint4(pack2(l[0], l[1]), pack2(l[2], l[3]), pack2(l[4], l[5]), pack2(l[6], l[7]));
-      } else {
-        a = *reinterpret_cast<const uint4*>(qrow + d0);
+    for (int j = 0; j < Tile<D>::KSTEPS; ++j) {
+      const int d0 = kstep_dim0<WIDE>(j, g);
+      uint4 a = make_uint4(0, 0, 0, 0), b = make_uint4(0, 0, 0, 0);
+      if (col < nh && d0 < D) {
+        if constexpr (SPLIT_Q) {
+          const float4 x0 = *reinterpret_cast<const float4*>(qrow + d0);
+          const float4 x1 = *reinterpret_cast<const float4*>(qrow + d0 + 4);
+          uint32_t h[8], l[8];
+          split_q<CT>(x0.x, h[0], l[0]);
+          split_q<CT>(x0.y, h[1], l[1]);
+          split_q<CT>(x0.z, h[2], l[2]);
+          split_q<CT>(x0.w, h[3], l[3]);
+          split_q<CT>(x1.x, h[4], l[4]);
+          split_q<CT>(x1.y, h[5], l[5]);
+          split_q<CT>(x1.z, h[6], l[6]);
+          split_q<CT>(x1.w, h[7], l[7]);
+          a = make_uint4(pack2(h[0], h[1]), pack2(h[2], h[3]), pack2(h[4], h[5]), pack2(h[6], h[7]));
+          b = make_uint4(pack2(l[0], l[1]), pack2(l[2], l[3]), pack2(l[4], l[5]), pack2(l[6], l[7]));
+        } else {
+          a = *reinterpret_cast<const uint4*>(qrow + d0);
+        }
       }
+      qa[j] = a;
+      if constexpr (SPLIT_Q) qb[j] = b;
     }
-    qa[j] = a;
-    if constexpr (SPLIT_Q) qb[j] = b;
   }
 }
 
@@ -721,12 +848,66 @@ __device__ __forceinline__ void load_query(const DecodeParams& p, int seq, int h
 // ctx is the context length of the lane's column (its ALiBi origin).
 // COLMASK: columns with col_on false take no part in this tile (their
 // scores are -inf), for tiles that serve only some of the columns.
+//
+// The online-softmax step shared by every cache type: scores sacc (lane
+// (g, col), register r = token vtok + r, head col) -> weights pr against the
+// running reference maximum, updating acc's maxima, sum and (on a raised
+// reference) its accumulators.  kpb / vpb / zero_v: the tile's masking state
+// as consume_tile describes it.
+template <int D, int BS, bool TAIL, bool COLMASK>
+__device__ __forceinline__ void softmax_tile(const DecodeParams& p, f32x4 sacc, int vtok, int t1, uint32_t ctx,
+                                             int g, float slope, int kpb, int vpb, bool zero_v, bool col_on,
+                                             WaveAcc<D>& acc, float (&pr)[4]) {
+  constexpr int DT = Tile<D>::DT;
+  float sc[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) sc[r] = sacc[r] * p.scale_log2;
+  if (p.alibi != nullptr) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sc[r] += slope * (float)(vtok + r - (int)ctx + 1);
+  }
+  if constexpr (COLMASK) {
+    if (!col_on) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sc[r] = -INFINITY;
+    }
+  }
+  if (TAIL || zero_v) {
+    // Lane (g, col) holds scores of tokens vtok..vtok+3 for head col; the K
+    // row of token tt0 + i was loaded by lane col = i.
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int krow_ok = __shfl(kpb, 4 * g + r, 16) >= 0;
+      sc[r] = (vtok + r < t1 && vpb >= 0 && krow_ok) ? sc[r] : -INFINITY;
+    }
+  } else if constexpr (BS >= kTile) {
+    if (vpb < 0) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sc[r] = -INFINITY;
+    }
+  }
+  const float mt = column_max(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
+  acc.m_max = fmaxf(acc.m_max, mt);
+  if (__any(mt > acc.m_run + kRescaleSlack)) {
+    const float m_new = fmaxf(acc.m_run, mt);
+    const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(acc.m_run - m_new);
+    acc.l_run *= alpha;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) acc.o[dt] *= alpha;
+    acc.m_run = m_new;
+  }
+  const float m_use = acc.m_run == -INFINITY ? 0.f : acc.m_run;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) pr[r] = fast_exp2(sc[r] - m_use);
+  acc.l_run += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+}
+
 template <class QT, class CT, int D, int BS, bool ROWS, bool TAIL, bool COLMASK = false>
-__device__ __forceinline__ void consume_tile(const DecodeParams& p, Tile<D, std::is_same<CT, FP8>::value>& t,
-                                             int tt0, int t1, uint32_t ctx, int g, int col,
-                                             const uint4 (&qa)[Tile<D>::KSTEPS],
-                                             const uint4 (&qb)[std::is_same<QT, F32>::value ? Tile<D>::KSTEPS : 1],
-                                             float slope, WaveAcc<D>& acc, bool col_on = true) {
+__device__ __forceinline__ void consume_tile_h(const DecodeParams& p, Tile<D, std::is_same<CT, FP8>::value>& t,
+                                               int tt0, int t1, uint32_t ctx, int g, int col,
+                                               const uint4 (&qa)[Tile<D>::KSTEPS],
+                                               const uint4 (&qb)[std::is_same<QT, F32>::value ? Tile<D>::KSTEPS : 1],
+                                               float slope, WaveAcc<D>& acc, bool col_on = true) {
   constexpr int KSTEPS = Tile<D>::KSTEPS;
   constexpr int DT = Tile<D>::DT;
   constexpr bool SPLIT_Q = std::is_same<QT, F32>::value;
@@ -777,48 +958,8 @@ __device__ __forceinline__ void consume_tile(const DecodeParams& p, Tile<D, std:
     if constexpr (SPLIT_Q) sacc = Mma<MT>::k32(t.k[j], qb[j], sacc);
   }
   // ---- online softmax (log2 domain) ----
-  float sc[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) sc[r] = sacc[r] * p.scale_log2;
-  if (p.alibi != nullptr) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) sc[r] += slope * (float)(vtok + r - (int)ctx + 1);
-  }
-  if constexpr (COLMASK) {
-    if (!col_on) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) sc[r] = -INFINITY;
-    }
-  }
-  if (TAIL || zero_v) {
-    // Lane (g, col) holds scores of tokens vtok..vtok+3 for head col; the K
-    // row of token tt0 + i was loaded by lane col = i.
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int krow_ok = __shfl(t.kpb, 4 * g + r, 16) >= 0;
-      sc[r] = (vtok + r < t1 && t.vpb >= 0 && krow_ok) ? sc[r] : -INFINITY;
-    }
-  } else if constexpr (BS >= kTile) {
-    if (t.vpb < 0) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) sc[r] = -INFINITY;
-    }
-  }
-  const float mt = column_max(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
-  acc.m_max = fmaxf(acc.m_max, mt);
-  if (__any(mt > acc.m_run + kRescaleSlack)) {
-    const float m_new = fmaxf(acc.m_run, mt);
-    const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(acc.m_run - m_new);
-    acc.l_run *= alpha;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) acc.o[dt] *= alpha;
-    acc.m_run = m_new;
-  }
-  const float m_use = acc.m_run == -INFINITY ? 0.f : acc.m_run;
   float pr[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) pr[r] = fast_exp2(sc[r] - m_use);
-  acc.l_run += (pr[0] + pr[1]) + (pr[2] + pr[3]);
+  softmax_tile<D, BS, TAIL, COLMASK>(p, sacc, vtok, t1, ctx, g, slope, t.kpb, t.vpb, zero_v, col_on, acc, pr);
   // ---- O^T += V^T * P^T ----
   const uint2 pp = make_uint2(pack_p<MT>(pr[0], pr[1]), pack_p<MT>(pr[2], pr[3]));
   if constexpr (COLMASK) {
@@ -834,6 +975,79 @@ __device__ __forceinline__ void consume_tile(const DecodeParams& p, Tile<D, std:
   }
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) acc.o[dt] = Mma<MT>::k16(t.v[dt], pp, acc.o[dt]);
+}
+
+// consume_tile for float32 caches (TileF32; paged layout, no column masks):
+// the same masking and softmax, with the scores and PV on
+// v_mfma_f32_16x16x4_f32.  Each product chain is split over four
+// accumulators so that consecutive MFMAs do not wait on each other.
+template <int D, int BS, bool TAIL>
+__device__ __forceinline__ void consume_tile_f32(const DecodeParams& p, TileF32<D>& t, int tt0, int t1, uint32_t ctx,
+                                                 int g, const uint4 (&qa)[Tile<D>::KSTEPS],
+                                                 const uint4 (&qb)[Tile<D>::KSTEPS], float slope, WaveAcc<D>& acc) {
+  constexpr int KM = TileF32<D>::KM;
+  constexpr int DT = TileF32<D>::DT;
+  const int vtok = tt0 + 4 * g;
+  bool zero_v = false;
+  if constexpr (TAIL) {
+    zero_v = true;
+  } else if constexpr (BS < kTile) {
+    zero_v = !__all(t.vpb >= 0 && t.kpb >= 0);
+  }
+  if (zero_v) {
+    // Masked tokens' V may hold anything (NaN included): zero it, since
+    // their weights are 0.
+    const bool ok = t.vpb >= 0;
+    const bool u0 = ok && vtok + 0 < t1, u1 = ok && vtok + 1 < t1;
+    const bool u2 = ok && vtok + 2 < t1, u3 = ok && vtok + 3 < t1;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      t.v[dt].x = u0 ? t.v[dt].x : 0.f;
+      t.v[dt].y = u1 ? t.v[dt].y : 0.f;
+      t.v[dt].z = u2 ? t.v[dt].z : 0.f;
+      t.v[dt].w = u3 ? t.v[dt].w : 0.f;
+    }
+  }
+  // ---- S^T = K * Q^T ----
+  f32x4 s4[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) s4[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int m = 0; m < KM; ++m) {
+    const float4 q = query_f32<D>(qa, qb, m);
+    s4[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(t.k[m].x, q.x, s4[0], 0, 0, 0);
+    s4[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(t.k[m].y, q.y, s4[1], 0, 0, 0);
+    s4[2] = __builtin_amdgcn_mfma_f32_16x16x4f32(t.k[m].z, q.z, s4[2], 0, 0, 0);
+    s4[3] = __builtin_amdgcn_mfma_f32_16x16x4f32(t.k[m].w, q.w, s4[3], 0, 0, 0);
+  }
+  const f32x4 sacc = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+  float pr[4];
+  softmax_tile<D, BS, TAIL, false>(p, sacc, vtok, t1, ctx, g, slope, t.kpb, t.vpb, zero_v, true, acc, pr);
+  // ---- O^T += V^T * P^T: MFMA r takes tokens 4g + r ----
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt) {
+    f32x4 o = acc.o[dt];
+    o = __builtin_amdgcn_mfma_f32_16x16x4f32(t.v[dt].x, pr[0], o, 0, 0, 0);
+    o = __builtin_amdgcn_mfma_f32_16x16x4f32(t.v[dt].y, pr[1], o, 0, 0, 0);
+    o = __builtin_amdgcn_mfma_f32_16x16x4f32(t.v[dt].z, pr[2], o, 0, 0, 0);
+    o = __builtin_amdgcn_mfma_f32_16x16x4f32(t.v[dt].w, pr[3], o, 0, 0, 0);
+    acc.o[dt] = o;
+  }
+}
+
+// Consumes one loaded tile (consume_tile_h for 16-bit and FP8 caches,
+// consume_tile_f32 for float32 caches).
+template <class QT, class CT, int D, int BS, bool ROWS, bool TAIL, bool COLMASK = false>
+__device__ __forceinline__ void consume_tile(const DecodeParams& p, TileOf<CT, D>& t, int tt0, int t1, uint32_t ctx,
+                                             int g, int col, const uint4 (&qa)[Tile<D>::KSTEPS],
+                                             const uint4 (&qb)[std::is_same<QT, F32>::value ? Tile<D>::KSTEPS : 1],
+                                             float slope, WaveAcc<D>& acc, bool col_on = true) {
+  if constexpr (std::is_same<CT, F32>::value) {
+    static_assert(!ROWS && !COLMASK, "float32 caches are read in the paged layout by the one-sequence kernels");
+    consume_tile_f32<D, BS, TAIL>(p, t, tt0, t1, ctx, g, qa, qb, slope, acc);
+  } else {
+    consume_tile_h<QT, CT, D, BS, ROWS, TAIL, COLMASK>(p, t, tt0, t1, ctx, g, col, qa, qb, slope, acc, col_on);
+  }
 }
 
 // load_query with the lane's own sequence and query head (columns of one
@@ -900,7 +1114,8 @@ __device__ __forceinline__ void stream_tiles(const DecodeParams& p, const typena
   constexpr int DT = Tile<D>::DT;
   constexpr int PT = WaveBlocks<BS, MAXT>::PER_TILE;
   constexpr bool F8 = std::is_same<CT, FP8>::value;
-  using TileT = Tile<D, F8>;
+  constexpr bool F32C = std::is_same<CT, F32>::value;
+  using TileT = TileOf<CT, D>;
   const int ntiles = (t1 - t0 + kTile - 1) / kTile;
   const int nfull = (t1 - t0) / kTile;  // tiles entirely inside [t0, t1)
   if (first >= ntiles) return;
@@ -911,7 +1126,7 @@ __device__ __forceinline__ void stream_tiles(const DecodeParams& p, const typena
   // landed, so reusing registers across the loop back-edge costs no drain.
   constexpr int NBUF = Prefetch<QT, D, BS>::kBuffers < MAXBUF ? Prefetch<QT, D, BS>::kBuffers : MAXBUF;
   static_assert(NBUF >= 2, "the prefetch loop needs at least two tile buffers");
-  constexpr int LOADS = KSTEPS + DT;
+  constexpr int LOADS = TileSel<CT, D>::kLoads;
   constexpr int AHEAD = (NBUF - 1) * LOADS;
   static_assert(AHEAD < 64, "vmcnt counts at most 63 outstanding loads");
   // s_waitcnt immediate (gfx9 encoding): vmcnt in bits 3:0 and 15:14,
@@ -933,6 +1148,9 @@ __device__ __forceinline__ void stream_tiles(const DecodeParams& p, const typena
       if constexpr (F8)
         load_tile_fp8<D, BS, kStreamCpol>(t, kbase, vbase, p.k_block_stride, p.v_block_stride, b0, b1, t0 + tile * kTile, g,
                              col);
+      else if constexpr (F32C)
+        load_tile_f32<D, BS, kStreamCpol>(t, kbase, vbase, p.k_block_stride, p.v_block_stride, b0, b1, t0 + tile * kTile,
+                                          g, col);
       else
         load_tile<D, BS, kStreamCpol>(t, kbase, vbase, p.k_block_stride, p.v_block_stride, b0, b1, t0 + tile * kTile, g, col);
     }
@@ -1900,8 +2118,8 @@ static hipError_t launch_persistent(const DecodeParams& p, hipStream_t stream, b
   if (!p.persistent) return hipSuccess;
   // The grouped kernel's two job buffers leave no register room (it would
   // spill) above head size 128 and for 8-token blocks at 112 and above;
-  // those keep the one-sequence kernel.
-  constexpr bool kGroupable = BS > 0 && D <= 128 && !(BS == 8 && D >= 112);
+  // those keep the one-sequence kernel, as do float32 caches.
+  constexpr bool kGroupable = BS > 0 && D <= 128 && !(BS == 8 && D >= 112) && !std::is_same<CT, F32>::value;
   if constexpr (kGroupable) {
     const hipError_t ge = launch_grouped<QT, CT, D, BS>(p, stream, launched);
     if (*launched || ge != hipSuccess) return ge;
@@ -1972,6 +2190,7 @@ static hipError_t launch_rows(const DecodeParams& p, hipStream_t stream) {
 }
 
 // FP8 caches: paged 5-D layout only, head sizes that are multiples of x = 16.
+// Float32 caches: paged 5-D layout only.
 template <class QT, class CT, int D>
 static hipError_t launch_layout(const DecodeParams& p, int block_size, hipStream_t stream, bool* ok) {
   if constexpr (std::is_same<CT, FP8>::value) {
@@ -1985,6 +2204,12 @@ static hipError_t launch_layout(const DecodeParams& p, int block_size, hipStream
       }
       return launch_bs<QT, CT, D>(p, block_size, stream, ok);
     }
+  } else if constexpr (std::is_same<CT, F32>::value) {
+    if (p.rows) {  // float32 caches: paged layout only
+      *ok = false;
+      return hipErrorInvalidValue;
+    }
+    return launch_bs<QT, CT, D>(p, block_size, stream, ok);
   } else {
     if (p.rows) return launch_rows<QT, CT, D>(p, stream);
     return launch_bs<QT, CT, D>(p, block_size, stream, ok);

@@ -23,9 +23,21 @@ int fail(int code, const std::string& msg) {
   return code;
 }
 
+// A failed HIP call also leaves its error as the thread's pending "last
+// error", which the next hipGetLastError() of any code on the thread (this
+// library's launch checks, torch's) would report as its own.  The status
+// returned here already carries it, so it is reset.
 int hip_fail(hipError_t e, const char* where) {
+  (void)hipGetLastError();
   return fail(PKV_ERR_HIP, std::string(where) + ": " + hipGetErrorString(e));
 }
+
+// Launches report failure only through hipGetLastError(), which returns the
+// thread's pending error whichever call left it.  Each entry point clears it
+// right before launching, so that a launch status describes that launch;
+// an error left pending by other code was returned by the call that caused
+// it.
+void clear_pending_error() { (void)hipGetLastError(); }
 
 int elem_bytes(int32_t dt) { return dt == PKV_F32 ? 4 : dt == PKV_FP8_E4M3 ? 1 : 2; }
 // Nonzero finite scale whose reciprocal is exact: a power of two whose
@@ -49,9 +61,6 @@ bool valid_block_size(int32_t b) { return b == 8 || b == 16 || b == 32; }
 
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-// Partition used for the single-pass (v1) semantics: 512 tokens, halved
-// while the grid would hold fewer than 2048 workgroups, doubled while one
-// sequence would need more than kMaxParts partitions.
 // Partition size of paged_attention_v1 on the partition path: the largest
 // (at most 4096 tokens, at least 256) that still gives one workgroup per CU
 // of MI355X (256).  Measured at 32K-128K contexts, fewer and longer
@@ -173,6 +182,7 @@ int pkv_reshape_and_cache(const void* key, const void* value, void* key_cache, v
   p.scales_pow2 = exact_reciprocal(k_scale) && exact_reciprocal(v_scale);
   p.k_inv = p.scales_pow2 ? 1.f / k_scale : 0.f;
   p.v_inv = p.scales_pow2 ? 1.f / v_scale : 0.f;
+  clear_pending_error();
   const hipError_t e = pkv::launch_reshape_and_cache(p, aligned, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "reshape_and_cache launch");
   return PKV_OK;
@@ -243,11 +253,13 @@ int paged_attention_impl(void* out, const void* query, const void* key_cache, co
   if (!valid_head_size(head_size) || !(valid_block_size(block_size) || (rows && block_size == 1)))
     return fail(PKV_ERR_UNSUPPORTED, "Unsupported head_size/block_size for paged_attention");
   const bool fp8 = cache_dtype == PKV_FP8_E4M3;
-  const bool pair_ok = (q_dtype == PKV_BF16 && cache_dtype == PKV_BF16) ||
-                       (q_dtype == PKV_F16 && cache_dtype == PKV_F16) ||
-                       (q_dtype == PKV_F32 && (cache_dtype == PKV_BF16 || cache_dtype == PKV_F16)) ||
-                       (fp8 && (q_dtype == PKV_BF16 || q_dtype == PKV_F16 || q_dtype == PKV_F32));
+  const bool pair_ok =
+      (q_dtype == PKV_BF16 && cache_dtype == PKV_BF16) || (q_dtype == PKV_F16 && cache_dtype == PKV_F16) ||
+      (q_dtype == PKV_F32 && (cache_dtype == PKV_BF16 || cache_dtype == PKV_F16 || cache_dtype == PKV_F32)) ||
+      (fp8 && (q_dtype == PKV_BF16 || q_dtype == PKV_F16 || q_dtype == PKV_F32));
   if (!pair_ok) return fail(PKV_ERR_UNSUPPORTED, "Unsupported query/cache dtype pair for paged_attention");
+  if (cache_dtype == PKV_F32 && rows)
+    return fail(PKV_ERR_UNSUPPORTED, "float32 caches are read in the paged layout");
   if (fp8 && (rows || head_size % 16 != 0))
     return fail(PKV_ERR_UNSUPPORTED, "FP8 caches are read in the paged layout with head_size a multiple of 16");
   if (fp8 && !(std::isfinite(k_scale) && std::isfinite(v_scale) && k_scale != 0.f && v_scale != 0.f))
@@ -271,11 +283,11 @@ int paged_attention_impl(void* out, const void* query, const void* key_cache, co
   const int64_t kbs = rows ? k_block_stride / block_size : k_block_stride;
   const int64_t vbs = rows ? v_block_stride / block_size : v_block_stride;
   // K: 16-byte loads; V: 8-byte loads in the paged layout, 16-byte loads of
-  // token rows (the same byte alignment for FP8 caches, whose wide tiles
-  // load 16 K codes and 8 V codes per lane).
+  // token rows and of float32 caches (the same byte alignment for FP8
+  // caches, whose wide tiles load 16 K codes and 8 V codes per lane).
   const int64_t cb = elem_bytes(cache_dtype);
   const int64_t k_align = 16;
-  const int64_t v_align = rows ? 16 : 8;
+  const int64_t v_align = (rows || cache_dtype == PKV_F32) ? 16 : 8;
   if (!aligned16(key_cache) || (kbs * cb) % k_align != 0 || (k_head_stride * cb) % k_align != 0 ||
       (reinterpret_cast<uintptr_t>(value_cache) % v_align) != 0 || (vbs * cb) % v_align != 0 ||
       (v_head_stride * cb) % v_align != 0)
@@ -343,6 +355,7 @@ int paged_attention_impl(void* out, const void* query, const void* key_cache, co
   bool ok = true;
   hipError_t e = hipErrorInvalidValue;
   const hipStream_t s = static_cast<hipStream_t>(stream);
+  clear_pending_error();
   if (fp8) {
     if (q_dtype == PKV_BF16)
       e = pkv::launch_decode_typed<pkv::BF16, pkv::FP8>(p, head_size, block_size, s, &ok);
@@ -350,7 +363,9 @@ int paged_attention_impl(void* out, const void* query, const void* key_cache, co
       e = pkv::launch_decode_typed<pkv::F16, pkv::FP8>(p, head_size, block_size, s, &ok);
     else
       e = pkv::launch_decode_typed<pkv::F32, pkv::FP8>(p, head_size, block_size, s, &ok);
-  } else if (q_dtype == PKV_BF16)
+  } else if (cache_dtype == PKV_F32)
+    e = pkv::launch_decode_typed<pkv::F32, pkv::F32>(p, head_size, block_size, s, &ok);
+  else if (q_dtype == PKV_BF16)
     e = pkv::launch_decode_typed<pkv::BF16, pkv::BF16>(p, head_size, block_size, s, &ok);
   else if (q_dtype == PKV_F16)
     e = pkv::launch_decode_typed<pkv::F16, pkv::F16>(p, head_size, block_size, s, &ok);
@@ -426,6 +441,7 @@ int pkv_copy_blocks(void* const* src_planes, void* const* dst_planes, int32_t nu
   p.src_blocks = src_blocks;
   p.dst_blocks = dst_blocks;
   p.block_bytes = block_bytes;
+  clear_pending_error();
   for (int32_t plane0 = 0; plane0 < num_planes; plane0 += pkv::kMaxCopyPlanes) {
     p.num_planes = std::min<int32_t>(pkv::kMaxCopyPlanes, num_planes - plane0);
     for (int32_t i = 0; i < p.num_planes; ++i) {
@@ -459,6 +475,7 @@ int pkv_convert_fp8(void* dst, const void* src, int64_t num_elements, float scal
     const uintptr_t d0 = reinterpret_cast<uintptr_t>(dst), d1 = d0 + (uintptr_t)num_elements * db;
     if (s0 < d1 && d0 < s1) return fail(PKV_ERR_INVALID, "dst and src overlap");
   }
+  clear_pending_error();
   const hipError_t e = pkv::launch_convert_fp8(dst, src, num_elements, scale, src_dtype, dst_dtype,
                                                static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return hip_fail(e, "convert_fp8 launch");

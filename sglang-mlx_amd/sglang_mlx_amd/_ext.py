@@ -157,9 +157,11 @@ def _check_paged_attention(query, key_cache, value_cache, block_tables, context_
     if not rows and key_cache.shape[4] != 16 // _ELEM_BYTES[key_cache.dtype]:
         raise ValueError("key_cache last dimension must be 16 / element size of the cache dtype")
     fp8 = cc == _lib.PKV_FP8_E4M3
-    if not (qc == cc and qc != _lib.PKV_F32) and not (qc == _lib.PKV_F32 and cc != _lib.PKV_F32) and not fp8:
+    if not (qc == cc or qc == _lib.PKV_F32 or fp8):
         raise ValueError(
             f"Unsupported query/cache dtype pair for paged_attention: {query.dtype}/{key_cache.dtype}")
+    if cc == _lib.PKV_F32 and rows:
+        raise ValueError("float32 caches are read in the paged layout")
     if fp8 and (rows or query.shape[2] % 16):
         raise ValueError("FP8 caches are read in the paged layout with head_size a multiple of 16")
     if not rows:

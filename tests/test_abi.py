@@ -69,7 +69,10 @@ def attn(noalloc=False, **kw):
     (dict(D=100), 2, "Unsupported head_size/block_size for paged_attention"),
     (dict(bs=64, max_blocks=1), 2, "Unsupported head_size/block_size for paged_attention"),
     (dict(qd=_lib.PKV_F16, cd=_lib.PKV_BF16), 2, "Unsupported query/cache dtype pair"),
-    (dict(qd=_lib.PKV_F32, cd=_lib.PKV_F32), 2, "Unsupported query/cache dtype pair"),
+    (dict(qd=_lib.PKV_BF16, cd=_lib.PKV_F32), 2, "Unsupported query/cache dtype pair"),
+    (dict(qd=_lib.PKV_F32, cd=_lib.PKV_F32, layout=_lib.PKV_LAYOUT_TOKEN_MAJOR), 2,
+     "float32 caches are read in the paged layout"),
+    (dict(qd=_lib.PKV_F32, cd=_lib.PKV_F32), 1, "null buffer"),
     (dict(ps=24), 1, "partition_size must be a positive multiple of 16"),
     (dict(ps=8192), 1, "partition_size must be a positive multiple of 16"),
     (dict(bs=32, max_blocks=2, ps=16), 1, "partition_size must be a positive multiple of 16 and of block_size"),

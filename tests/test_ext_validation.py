@@ -182,3 +182,18 @@ def test_fp8_token_major_append_needs_rows_of_eight():
     cache = torch.zeros(8, 2, 8, dtype=torch.uint8)
     with pytest.raises(RuntimeError, match="GPU-only"):
         kernels.reshape_and_cache(key, key.clone(), cache, cache.clone(), torch.zeros(3, dtype=torch.int32))
+
+
+def test_float32_caches():
+    # (float32 query, float32 cache) is the reference's (float, float) pair:
+    # accepted in the paged layout (x = 4), rejected for token rows.
+    q = torch.zeros(2, 8, 64)
+    kc = torch.zeros(6, 2, 16, 16, 4)
+    vc = torch.zeros(6, 2, 64, 16)
+    with pytest.raises(RuntimeError, match="GPU-only"):
+        kernels.paged_attention_v1(**pa_args(query=q, key_cache=kc, value_cache=vc))
+    with pytest.raises(ValueError, match="Unsupported query/cache dtype pair"):
+        kernels.paged_attention_v1(**pa_args(query=q.half(), key_cache=kc, value_cache=vc))
+    with pytest.raises(ValueError, match="float32 caches are read in the paged layout"):
+        kernels.paged_attention_v1(**rows_args(query=q, key_cache=torch.zeros(96, 2, 64),
+                                               value_cache=torch.zeros(96, 2, 64)))

@@ -40,3 +40,30 @@ def test_bad_device_raises_runtime_error():
         _ext.get_device_attribute(HIP_ATTR_MULTIPROCESSOR_COUNT, torch.cuda.device_count() + 3)
     with pytest.raises(RuntimeError, match="hipDeviceGetAttribute"):
         _ext.get_max_shared_memory_per_block_device_attribute(torch.cuda.device_count() + 3)
+    # The failed query leaves no pending HIP error behind: the library's
+    # next launch and torch's next kernel both succeed.
+    src = torch.arange(64, dtype=torch.float32, device="cuda")
+    dst = torch.empty(64, dtype=torch.uint8, device="cuda")
+    _ext.convert_fp8(dst, src, 1.0)
+    y = src * 2
+    torch.cuda.synchronize()
+    assert y[5].item() == 10.0 and dst[1].item() == 0x38   # 1.0 in E4M3
+
+
+def test_launch_status_ignores_an_earlier_pending_error():
+    # A HIP call outside the library fails and leaves its error pending; the
+    # library's next launch reports its own success and leaves nothing
+    # pending for torch.  (HIP is opened by its soname, so this is the
+    # runtime torch already loaded, not a second copy.)
+    import ctypes
+    hip = ctypes.CDLL("libamdhip64.so.7")
+    src = torch.ones(64, dtype=torch.float32, device="cuda")
+    dst = torch.empty(64, dtype=torch.uint8, device="cuda")
+    torch.cuda.synchronize()
+    n = ctypes.c_int(0)
+    assert hip.hipDeviceGetAttribute(ctypes.byref(n), HIP_ATTR_MULTIPROCESSOR_COUNT,
+                                     torch.cuda.device_count() + 3) != 0
+    _ext.convert_fp8(dst, src, 1.0)
+    y = src + 1
+    torch.cuda.synchronize()
+    assert (dst == 0x38).all() and (y == 2).all()
