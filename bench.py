@@ -78,7 +78,8 @@ def parse_args():
     ap.add_argument("--no-radix", action="store_true", help="skip the radix-shared decode measurement")
     ap.add_argument("--no-rows", action="store_true", help="skip the token-row (MHATokenPool) decode measurement")
     ap.add_argument("--no-fp8", action="store_true", help="skip the FP8-cache decode measurement")
-    ap.add_argument("--only", choices=["decode", "append", "copy", "splitk", "radix", "radix_fp8", "rows", "fp8"],
+    ap.add_argument("--no-sweep", action="store_true", help="skip the batch-size sweep of the decode layer")
+    ap.add_argument("--only", choices=["decode", "append", "copy", "splitk", "radix", "radix_fp8", "rows", "fp8", "sweep"],
                     help="run one leg and print its own short JSON line (for counter collection under "
                          "rocprofv3 --pmc): the decode layer, the token-major append, or a plain 1 GiB device "
                          "copy whose FETCH_SIZE / WRITE_SIZE calibrate the counters")
@@ -345,6 +346,36 @@ def bench_fp8(dev, kernels, layers: int = 4, steps: int = 100, warmup: int = 10)
     return out
 
 
+def bench_batch_sweep(dev, kernels, batches=(8, 16, 32, 48, 63, 64, 96, 128), launches: int = 24):
+    """The Llama-3-8B decode layer (32 q / 8 kv heads, D128, bs16, ctx
+    U[512, 4096], bf16) through paged_attention_v1 at several batch sizes,
+    each a HIP graph of `launches` calls over layer pools rotated to exceed
+    the Infinity Cache (median of 5 replays)."""
+    Hq, Hkv, D, bs = 32, 8, 128, 16
+    scale = 1.0 / math.sqrt(D)
+    rows = []
+    for B in batches:
+        pool_bytes = int(B * 2304 * Hkv * D * 2 * 2 * 1.1)
+        layers = max(2, -(-800_000_000 // pool_bytes))
+        inp = decode_inputs(1003, B=B, Hq=Hq, Hkv=Hkv, D=D, bs=bs, ctx_lo=512, ctx_hi=4096, layers=layers, dev=dev)
+        nbytes = decode_bytes(inp["ctx_np"], B, Hq, Hkv, D, bs)
+
+        def step(i):
+            kc, vc = inp["pools"][i % layers]
+            return kernels.paged_attention_v1(inp["q"], kc, vc, inp["bt"], inp["ctx"], Hkv, scale, bs, 4096)
+
+        ms = graph_launch_ms(step, launches)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        rows.append(dict(batch=B, us=round(ms * 1e3, 2), bytes_per_launch=nbytes, gbs=round(gbs, 1),
+                         frac=round(gbs / PEAK_GBS, 4), max_ctx=int(inp["ctx_np"].max())))
+        del inp
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+    return dict(workload="llama3-8b paged decode layer at several batch sizes: 32 q / 8 kv heads, D128, bs16, "
+                         "ctx U[512,4096] (seed 1003), bf16", rows=rows,
+                method=f"HIP graph of {launches} calls over rotated pools (> 800 MB), median of 5 replays")
+
+
 def bench_append(dev, kernels, sources: int = 24, pools: int = 4, launches: int = 96):
     """Append workload: 4096 tokens, 8 KV heads, D 128, bf16, 65,536 slots
     (4096 blocks of 16), unique random slots (slot 0 reserved), 5% = -1."""
@@ -517,6 +548,8 @@ def only_leg(args, dev, kernels):
         print(json.dumps(dict(leg="rows", **bench_rows(dev, kernels))))
     elif args.only == "fp8":
         print(json.dumps(dict(leg="fp8", **bench_fp8(dev, kernels))))
+    elif args.only == "sweep":
+        print(json.dumps(dict(leg="sweep", **bench_batch_sweep(dev, kernels))))
     else:
         n = 1 << 30
         src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
@@ -598,6 +631,8 @@ def main():
         line["token_rows"] = bench_rows(dev, kernels)
     if not args.no_fp8:
         line["fp8_kv"] = bench_fp8(dev, kernels)
+    if not args.no_sweep:
+        line["batch_sweep"] = bench_batch_sweep(dev, kernels)
     if not args.no_cpu:
         line["cpu_baseline"] = bench_cpu(res, args.cpu_budget)
     else:

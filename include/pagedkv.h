@@ -133,7 +133,7 @@ size_t pkv_paged_attention_workspace_size(int32_t num_seqs, int32_t num_heads,
  *                      partition_size tokens, merged by log-sum-exp.  Must be
  *                      a multiple of 16 and of block_size, at most 4096.
  * Launches (all on `stream`): for partition_size = 0, contexts of at most
- * 16384 tokens and at least two (sequence, KV head) items per resident
+ * 16384 tokens and at least one (sequence, KV head) item per resident
  * workgroup, one persistent kernel that gives each item to one workgroup,
  * longest contexts first; otherwise a partition kernel, plus a log-sum-exp
  * merge kernel when a sequence has more than one partition.

@@ -40,6 +40,8 @@
 // reference's single softmax.
 #pragma once
 
+#include <algorithm>
+
 #include "pkv_fp8.h"
 #include "pkv_launch.h"
 
@@ -83,6 +85,29 @@ constexpr float kRescaleSlack = 8.f;
 
 #ifndef PKV_NBUF
 #define PKV_NBUF 4
+#endif
+#ifndef PKV_PAD_ZERO
+#define PKV_PAD_ZERO 1
+#endif
+#ifndef PKV_PART_NBUF
+#define PKV_PART_NBUF 2
+#endif
+// Partitions per wavefront and step of the merge kernel (head sizes up to
+// 128), and the partition-kernel grids (in workgroups per CU) that get eight
+// wavefronts per workgroup.
+#ifndef PKV_MERGE_U
+#define PKV_MERGE_U 32
+#endif
+#ifndef PKV_PART_SMALL_GRID
+#define PKV_PART_SMALL_GRID 1
+#endif
+// The one-sequence persistent kernel is used from PKV_PERSIST_MIN4 / 4
+// (sequence, unit) items per resident workgroup: from one item each, where
+// the longest-first order gives the longest items a workgroup of their own.
+// (From two, the Llama-3-8B layer at 48 and 63 sequences fell to the
+// partition kernel: 97.3 and 109.2 us against 76.6 and 95.9 us persistent.)
+#ifndef PKV_PERSIST_MIN4
+#define PKV_PERSIST_MIN4 4
 #endif
 
 // Query element pair -> (hi, lo) words of the cache type; q = hi + lo to
@@ -741,6 +766,16 @@ template <int BS, int MAXT> struct WaveBlocks {
       v[c] = b;
     }
   }
+  // Block of entry e, for a different e in each lane (entries past the
+  // array read entry e % 64 of the first register; the caller ignores them).
+  __device__ __forceinline__ int fetch(int e) const {
+    const int c = e >> 6;
+    int x = v[0];
+#pragma unroll
+    for (int i = 1; i < N; ++i)
+      if (c == i) x = v[i];
+    return __shfl(x, e & 63);
+  }
   // Block of entry e (wave-uniform e).
   __device__ __forceinline__ int get(int e) const {
     const int c = e >> 6, l = e & 63;
@@ -847,7 +882,10 @@ __device__ __forceinline__ void load_query(const DecodeParams& p, int seq, int h
 // block's loads already returned zero, so only its scores need masking.
 // ctx is the context length of the lane's column (its ALiBi origin).
 // COLMASK: columns with col_on false take no part in this tile (their
-// scores are -inf), for tiles that serve only some of the columns.
+// scores are -inf), for tiles that serve only some of the columns; check_v
+// says whether any column the caller will write may be off, in which case a
+// tile with a non-finite V element keeps the off columns' accumulators out
+// of the PV product (0 * inf would be NaN).
 //
 // The online-softmax step shared by every cache type: scores sacc (lane
 // (g, col), register r = token vtok + r, head col) -> weights pr against the
@@ -907,7 +945,8 @@ __device__ __forceinline__ void consume_tile_h(const DecodeParams& p, Tile<D, st
                                                int tt0, int t1, uint32_t ctx, int g, int col,
                                                const uint4 (&qa)[Tile<D>::KSTEPS],
                                                const uint4 (&qb)[std::is_same<QT, F32>::value ? Tile<D>::KSTEPS : 1],
-                                               float slope, WaveAcc<D>& acc, bool col_on = true) {
+                                               float slope, WaveAcc<D>& acc, bool col_on = true,
+                                               bool check_v = true) {
   constexpr int KSTEPS = Tile<D>::KSTEPS;
   constexpr int DT = Tile<D>::DT;
   constexpr bool SPLIT_Q = std::is_same<QT, F32>::value;
@@ -963,8 +1002,8 @@ __device__ __forceinline__ void consume_tile_h(const DecodeParams& p, Tile<D, st
   // ---- O^T += V^T * P^T ----
   const uint2 pp = make_uint2(pack_p<MT>(pr[0], pr[1]), pack_p<MT>(pr[2], pr[3]));
   if constexpr (COLMASK) {
-    if constexpr (!F8) v_special = v_nonfinite<MT, D>(t);
-    if (v_special) {
+    if constexpr (!F8) v_special = check_v && v_nonfinite<MT, D>(t);
+    if (v_special && check_v) {
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
         const f32x4 r = Mma<MT>::k16(t.v[dt], pp, acc.o[dt]);
@@ -1041,12 +1080,14 @@ template <class QT, class CT, int D, int BS, bool ROWS, bool TAIL, bool COLMASK 
 __device__ __forceinline__ void consume_tile(const DecodeParams& p, TileOf<CT, D>& t, int tt0, int t1, uint32_t ctx,
                                              int g, int col, const uint4 (&qa)[Tile<D>::KSTEPS],
                                              const uint4 (&qb)[std::is_same<QT, F32>::value ? Tile<D>::KSTEPS : 1],
-                                             float slope, WaveAcc<D>& acc, bool col_on = true) {
+                                             float slope, WaveAcc<D>& acc, bool col_on = true,
+                                             bool check_v = true) {
   if constexpr (std::is_same<CT, F32>::value) {
     static_assert(!ROWS && !COLMASK, "float32 caches are read in the paged layout by the one-sequence kernels");
     consume_tile_f32<D, BS, TAIL>(p, t, tt0, t1, ctx, g, qa, qb, slope, acc);
   } else {
-    consume_tile_h<QT, CT, D, BS, ROWS, TAIL, COLMASK>(p, t, tt0, t1, ctx, g, col, qa, qb, slope, acc, col_on);
+    consume_tile_h<QT, CT, D, BS, ROWS, TAIL, COLMASK>(p, t, tt0, t1, ctx, g, col, qa, qb, slope, acc, col_on,
+                                                       check_v);
   }
 }
 
@@ -1138,13 +1179,20 @@ __device__ __forceinline__ void stream_tiles(const DecodeParams& p, const typena
   };
   using Full = std::integral_constant<bool, false>;
   using Tail = std::integral_constant<bool, true>;
-  auto load = [&](TileT& t, int tile) {
+  // pad: a load past the wavefront's last full tile, issued only to keep
+  // the loads per iteration fixed.  With blocks of 16 and more it gets the
+  // zero-sized buffer resource of a masked block, so it counts towards the
+  // wait like any other load but reads nothing.
+  auto load = [&](TileT& t, int tile, bool pad) {
     if constexpr (ROWS) {
       blk.template load_tile<D>(t, p, kbase, vbase, tile, (tile - first) / NW, g, col);
     } else {
       const int k = (tile - first) / NW;
-      const int b0 = blk.get(k * PT);
-      const int b1 = PT == 2 ? blk.get(k * PT + 1) : b0;
+      int b0 = blk.get(k * PT);
+      int b1 = PT == 2 ? blk.get(k * PT + 1) : b0;
+      if constexpr (BS >= kTile && PKV_PAD_ZERO) {
+        if (pad) b0 = b1 = -1;
+      }
       if constexpr (F8)
         load_tile_fp8<D, BS, kStreamCpol>(t, kbase, vbase, p.k_block_stride, p.v_block_stride, b0, b1, t0 + tile * kTile, g,
                              col);
@@ -1158,17 +1206,17 @@ __device__ __forceinline__ void stream_tiles(const DecodeParams& p, const typena
 
   // Full tiles: NBUF register sets, the loads of the wavefront's tile
   // i + NW*(NBUF-1) issued before tile i is consumed, so each wavefront keeps
-  // NBUF - 1 tiles in flight.  Past its last full tile a wavefront re-reads
-  // that tile (in bounds) so that every iteration issues the same loads; with
-  // the nt policy its lines need not still be in L2, so each such repeat may
-  // fetch up to one tile from HBM again (NBUF - 1 per wavefront and item).  (Driving the loop by the tile index rather than a 0-based
+  // NBUF - 1 tiles in flight.  Past its last full tile a wavefront still
+  // issues a tile's loads per iteration so that every iteration waits for
+  // the same count: zero-sized ones with blocks of 16 and more (see load),
+  // otherwise re-reads of its last tile (in bounds).  (Driving the loop by the tile index rather than a 0-based
   // per-wavefront counter keeps the compiler's register allocation of the
   // rotating tile sets tight.)
   if (first < nfull) {
     const int last = first + ((nfull - 1 - first) / NW) * NW;
     TileT t[NBUF];
 #pragma unroll
-    for (int b = 0; b < NBUF - 1; ++b) load(t[b], min(first + b * NW, last));
+    for (int b = 0; b < NBUF - 1; ++b) load(t[b], min(first + b * NW, last), first + b * NW > last);
     int tile = first;
     while (true) {
 #pragma unroll
@@ -1178,7 +1226,7 @@ __device__ __forceinline__ void stream_tiles(const DecodeParams& p, const typena
         // siblings busy with MFMA work: 106.2 against 106.6 us at the
         // Llama-3-8B layer, same process (the FP8 layer is unchanged).
         __builtin_amdgcn_s_setprio(1);
-        load(t[(b + NBUF - 1) % NBUF], min(tile + (NBUF - 1) * NW, last));
+        load(t[(b + NBUF - 1) % NBUF], min(tile + (NBUF - 1) * NW, last), tile + (NBUF - 1) * NW > last);
         __builtin_amdgcn_s_setprio(0);
         __builtin_amdgcn_s_waitcnt(kWaitAhead);
         consume(Full{}, t[b], t0 + tile * kTile);
@@ -1191,7 +1239,7 @@ __device__ __forceinline__ void stream_tiles(const DecodeParams& p, const typena
   // The tile that crosses t1, if this wavefront owns it.
   if (nfull < ntiles && nfull >= first && (nfull - first) % NW == 0) {
     TileT tt;
-    load(tt, nfull);
+    load(tt, nfull, false);
     consume(Tail{}, tt, t0 + nfull * kTile);
   }
 }
@@ -1407,7 +1455,8 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_part_kernel(DecodeParams
   const CS* vbase = static_cast<const CS*>(p.v_cache) + (int64_t)kvh * p.v_head_stride;
   // Two tile buffers: fewer registers, more resident workgroups per CU
   // (measured 1-4% faster than three or four at 32K-128K contexts).
-  stream_tiles<QT, CT, D, BS, NW, MAXT, 2>(p, kbase, vbase, blk, t0, t1, ctx, wave, g, col, qa, qb, slope, acc);
+  stream_tiles<QT, CT, D, BS, NW, MAXT, PKV_PART_NBUF>(p, kbase, vbase, blk, t0, t1, ctx, wave, g, col, qa, qb, slope,
+                                                      acc);
 
   float M, L;
   merge_waves<D, NW>(acc, s_red, s_m, s_l, wave, lane, g, col, M, L);
@@ -1540,12 +1589,18 @@ __global__ __launch_bounds__(64 * kPartWaves) void paged_decode_rows_kernel(Deco
 #ifndef PKV_FP8_NBUF
 #define PKV_FP8_NBUF 2
 #endif
+#ifndef PKV_PAGED_WAVES
+#define PKV_PAGED_WAVES 8
+#endif
+#ifndef PKV_PAGED_NBUF
+#define PKV_PAGED_NBUF 2
+#endif
 template <int D, bool ROWS = false, bool F8 = false> struct Persist {
   // Wavefronts per workgroup: two per SIMD while the register budget allows
   // (head sizes up to 128), one above.
-  static constexpr int kWaves = D <= 128 ? (ROWS ? PKV_ROWS_WAVES : 8) : 4;
+  static constexpr int kWaves = D <= 128 ? (ROWS ? PKV_ROWS_WAVES : PKV_PAGED_WAVES) : 4;
   // Tile buffers per wavefront.
-  static constexpr int kMaxBuf = ROWS ? PKV_ROWS_NBUF : F8 ? PKV_FP8_NBUF : 2;
+  static constexpr int kMaxBuf = ROWS ? PKV_ROWS_NBUF : F8 ? PKV_FP8_NBUF : PKV_PAGED_NBUF;
 };
 
 // Longest-first rank of the sequences (ties by index) into s_order, when
@@ -1706,8 +1761,11 @@ __global__ __launch_bounds__(64 * (Persist<D, BS == 0>::kWaves)) void paged_deco
 // same; what sharing saves is loads.  Items are ranked and dealt like the
 // persistent kernel's (groups of S sequences in longest-first order).
 // ---------------------------------------------------------------------------
-constexpr int kGroupSeqs = 4;       // sequences per item
-constexpr int kGroupMaxSeq = 8192;  // longest context (block ids in registers)
+#ifndef PKV_GROUP_MAXSEQ
+#define PKV_GROUP_MAXSEQ 8192
+#endif
+constexpr int kGroupSeqs = 4;                   // sequences per item
+constexpr int kGroupMaxSeq = PKV_GROUP_MAXSEQ;  // longest context (block ids in registers)
 
 template <int S> struct GroupItem {
   int kvh;
@@ -1715,9 +1773,29 @@ template <int S> struct GroupItem {
   uint32_t ctx[S];  // 0 unless live
 };
 
-template <class QT, class CT, int D, int BS, int S>
-__global__ __launch_bounds__(64 * Persist<D>::kWaves) void paged_decode_group_kernel(DecodeParams p) {
-  constexpr int NW = Persist<D>::kWaves;
+// Wavefronts per workgroup and tile buffers per wavefront of the grouped
+// kernel.  Measured on the radix-shared B256 workload (job iterator of the
+// previous form, same process): eight wavefronts with two buffers 105 us;
+// four wavefronts (one per SIMD, registers for a deeper ring) 157-160 us
+// with 3, 4, 5 or 6 buffers alike.  More tiles in flight did not help; a
+// second wavefront per SIMD to overlap each job's dependent instructions
+// did.  Counters then showed 271 VALU and 128 SALU instructions per job
+// against 82 and 48 per tile in the one-sequence kernel (same 12 MFMAs and
+// 12 loads), which the per-item job list below removes.
+#ifndef PKV_GROUP_WAVES
+#define PKV_GROUP_WAVES 8
+#endif
+#ifndef PKV_GROUP_NBUF
+#define PKV_GROUP_NBUF 2
+#endif
+// Workgroups launched per CU (at most what fits).
+#ifndef PKV_GROUP_PER_CU
+#define PKV_GROUP_PER_CU 1
+#endif
+
+template <class QT, class CT, int D, int BS, int S, int NW, int NB>
+__global__ __launch_bounds__(64 * NW) void paged_decode_group_kernel(DecodeParams p) {
+  static_assert(NB >= 2, "the job pipeline needs at least two tile buffers");
   constexpr int NT = 64 * NW;
   constexpr int KSTEPS = Tile<D>::KSTEPS;
   constexpr int DT = Tile<D>::DT;
@@ -1730,14 +1808,19 @@ __global__ __launch_bounds__(64 * Persist<D>::kWaves) void paged_decode_group_ke
   using CS = typename Elem<CT>::storage;
   using MT = typename MmaOf<QT, CT>::type;
   constexpr int LOADS = KSTEPS + DT;
-  static_assert(LOADS < 64, "vmcnt counts at most 63 outstanding loads");
-  constexpr int kWaitAhead = (LOADS & 15) | ((LOADS >> 4) << 14) | (7 << 4) | (15 << 8);
+  constexpr int AHEAD = (NB - 1) * LOADS;
+  static_assert(AHEAD < 64, "vmcnt counts at most 63 outstanding loads");
+  constexpr int kWaitAhead = (AHEAD & 15) | ((AHEAD >> 4) << 14) | (7 << 4) | (15 << 8);
 
-  __shared__ float4 s_red[2][NW][DT][64];
-  __shared__ float s_m[2][NW][16];
-  __shared__ float s_l[2][NW][16];
+  // Each wavefront's tiles of an item are its lanes (one tile per lane) when
+  // the job list is built.
+  static_assert(MAXT <= 64, "the job list takes one lane per tile of the wavefront");
+  __shared__ float4 s_red[NW][DT][64];
+  __shared__ float s_m[NW][16];
+  __shared__ float s_l[NW][16];
   __shared__ __align__(16) uint32_t s_ctx[kPersistMaxOrder];
   __shared__ int32_t s_order[kPersistMaxOrder];
+  __shared__ int4 s_jobs[NW][MAXT * S];  // per wavefront: the item's job list
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1798,7 +1881,6 @@ __global__ __launch_bounds__(64 * Persist<D>::kWaves) void paged_decode_group_ke
   // Each item's block ids, queries and slopes are loaded at its start (as
   // in the one-sequence persistent kernel, where loading them an item ahead
   // measured slower).
-  int buf = 0;
   for (int k = 0;; ++k) {
     const int rank = rank_of(k);
     if (rank >= total) break;
@@ -1815,11 +1897,18 @@ __global__ __launch_bounds__(64 * Persist<D>::kWaves) void paged_decode_group_ke
     int nt[S];  // tiles per sequence (0: not live)
     int maxnt = 0;
     uint32_t minctx = 0xffffffffu;
+    int first_live = -1;
+    bool all_live = true;  // every sequence slot of the item holds a live sequence
 #pragma unroll
     for (int i = 0; i < S; ++i) {
       nt[i] = ((int)it.ctx[i] + kTile - 1) / kTile;
       maxnt = max(maxnt, nt[i]);
-      if (it.ctx[i] != 0) minctx = min(minctx, it.ctx[i]);
+      if (it.ctx[i] != 0) {
+        minctx = min(minctx, it.ctx[i]);
+        if (first_live < 0) first_live = i;
+      } else {
+        all_live = false;
+      }
     }
     int lane_seq;
     uint32_t lane_ctx;
@@ -1828,67 +1917,92 @@ __global__ __launch_bounds__(64 * Persist<D>::kWaves) void paged_decode_group_ke
     const CS* kbase = static_cast<const CS*>(p.k_cache) + (int64_t)it.kvh * p.k_head_stride;
     const CS* vbase = static_cast<const CS*>(p.v_cache) + (int64_t)it.kvh * p.v_head_stride;
 
-    // Job = (position n in this wavefront's tile order, its tile index kk,
-    // sequence slot i, or -1 for a shared tile); kk < 0 marks the end.  All
-    // wave-uniform.  The wavefront takes its K tiles from both ends in turn
-    // (0, K-1, 1, K-2, ...): a shared prefix then alternates with private
-    // tails, so L2-served and HBM-served loads overlap instead of every
-    // workgroup reading its prefix first and its tails last.
-    struct Job {
-      int n, kk, i;
-    };
-    const int K = maxnt > wave ? (maxnt - 1 - wave) / NW + 1 : 0;
-    auto kk_of = [&](int n) { return (n & 1) ? K - 1 - (n >> 1) : (n >> 1); };
-    auto block_of = [&](int i, int e) {
-      int b = blk[0].get(e);
+    // Job list of this wavefront, built once per item: lane n describes
+    // the wavefront's tile kk(n) -- taken from both ends in turn (0, K-1,
+    // 1, K-2, ...), so that the shared prefix alternates with the private
+    // tails and L2-served and HBM-served loads overlap.  A tile is
+    //   * shared: every live sequence maps it to the same block(s) and holds
+    //     all 16 of its tokens -- one job that feeds every column, so a
+    //     radix-shared prefix is read once per S sequences;
+    //   * otherwise one job per sequence that reaches it, with only that
+    //     sequence's columns active.
+    // A wave prefix sum of the lanes' job counts places each lane's jobs in
+    // the wavefront's LDS list: (block of tokens 0-7, block of tokens 8-15,
+    // kk | (sequence slot + 1, 0 = shared) << 8 | valid tokens << 16).
+    const int K = maxnt > wave ? (maxnt - 1 - wave) / NW + 1 : 0;  // tiles of this wavefront
+    int njobs = 0;
+    if (K > 0) {
+      const bool has = lane < K;
+      const int kk = (lane & 1) ? K - 1 - (lane >> 1) : (lane >> 1);
+      const int tt0 = (wave + kk * NW) * kTile;
+      int b0[S], b1[S];
 #pragma unroll
-      for (int s2 = 1; s2 < S; ++s2)
-        if (i == s2) b = blk[s2].get(e);
-      return b;
-    };
-    auto job_at = [&](int n) -> Job {
-      if (n >= K) return Job{n, -1, 0};
-      const int kk = kk_of(n);
-      const int tile = wave + kk * NW;
-      bool shared = (uint32_t)(tile + 1) * kTile <= minctx;
-      int first_live = -1, b0 = 0, b1 = 0;
+      for (int i = 0; i < S; ++i) {
+        b0[i] = blk[i].fetch(kk * PT);
+        b1[i] = PT == 2 ? blk[i].fetch(kk * PT + 1) : b0[i];
+      }
+      bool shared = tt0 + kTile <= (int)minctx;
+      int fb0 = 0, fb1 = 0;
 #pragma unroll
       for (int i = 0; i < S; ++i) {
         if (it.ctx[i] == 0) continue;
-        const int c0 = block_of(i, kk * PT), c1 = PT == 2 ? block_of(i, kk * PT + 1) : c0;
-        if (first_live < 0) {
-          first_live = i;
-          b0 = c0;
-          b1 = c1;
+        if (i == first_live) {
+          fb0 = b0[i];
+          fb1 = b1[i];
         } else {
-          shared = shared && c0 == b0 && c1 == b1;
+          shared = shared && b0[i] == fb0 && b1[i] == fb1;
         }
       }
-      if (shared) return Job{n, kk, -1};
+      int cnt = 0;
+      if (has) {
+        if (shared) {
+          cnt = 1;
+        } else {
 #pragma unroll
-      for (int i = 0; i < S; ++i)
-        if (tile < nt[i]) return Job{n, kk, i};
-      return Job{n, -1, 0};  // not reached: tile < maxnt
-    };
-    auto next_job = [&](Job j) -> Job {
-      if (j.i >= 0) {
-        const int tile = wave + j.kk * NW;
-#pragma unroll
-        for (int i = 0; i < S; ++i)
-          if (i > j.i && tile < nt[i]) return Job{j.n, j.kk, i};
+          for (int i = 0; i < S; ++i) cnt += tt0 < (int)it.ctx[i];
+        }
       }
-      return job_at(j.n + 1);
-    };
-    auto load_job = [&](TileT& t, Job j) {
-      const int sel = j.i >= 0 ? j.i : [&] {
-        int f = 0;
+      int incl = cnt;  // inclusive prefix sum over the lanes
 #pragma unroll
-        for (int i = S - 1; i >= 0; --i)
-          if (it.ctx[i] != 0) f = i;
-        return f;
-      }();
-      const int b0 = block_of(sel, j.kk * PT);
-      const int b1 = PT == 2 ? block_of(sel, j.kk * PT + 1) : b0;
+      for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(incl, o);
+        incl += lane >= o ? y : 0;
+      }
+      njobs = __builtin_amdgcn_readlane(incl, 63);
+      int4* list = s_jobs[wave];
+      int at = incl - cnt;
+      if (has) {
+        if (shared) {
+          list[at] = make_int4(fb0, fb1, kk | (kTile << 16), 0);
+        } else {
+#pragma unroll
+          for (int i = 0; i < S; ++i) {
+            if (tt0 < (int)it.ctx[i]) {
+              const int ntok = min(kTile, (int)it.ctx[i] - tt0);
+              list[at++] = make_int4(b0[i], b1[i], kk | ((i + 1) << 8) | (ntok << 16), 0);
+            }
+          }
+        }
+      }
+    }
+    // The list is read back by every lane of the same wavefront only: the
+    // wavefront's LDS operations complete in order, and the barrier keeps
+    // the compiler from moving the reads above the writes.
+    __builtin_amdgcn_wave_barrier();
+    struct Job {
+      int b0, b1, kk, i, ntok;  // i = -1: shared; kk < 0: none
+    };
+    // Entry j of the list as read from LDS (every lane reads the same
+    // entry), and as a wave-uniform job.
+    auto entry_at = [&](int j) -> int4 { return s_jobs[wave][j < njobs ? j : 0]; };
+    auto job_of = [&](int j, int4 e) -> Job {
+      if (j >= njobs) return Job{0, 0, -1, -1, 0};
+      const int meta = __builtin_amdgcn_readfirstlane(e.z);
+      return Job{__builtin_amdgcn_readfirstlane(e.x), PT == 2 ? __builtin_amdgcn_readfirstlane(e.y) : 0,
+                 meta & 0xff, ((meta >> 8) & 0xff) - 1, meta >> 16};
+    };
+    auto load_job = [&](TileT& t, const Job& j) {
+      const int b0 = j.b0, b1 = PT == 2 ? j.b1 : j.b0;
       const int tt0 = (wave + j.kk * NW) * kTile;
       // A private job's tile is read once (nt, as in stream_tiles); a shared
       // tile keeps the default policy, as the other items of its KV head
@@ -1906,43 +2020,61 @@ __global__ __launch_bounds__(64 * Persist<D>::kWaves) void paged_decode_group_ke
           load_tile<D, BS>(t, kbase, vbase, p.k_block_stride, p.v_block_stride, b0, b1, tt0, g, col);
       }
     };
-    auto consume_job = [&](TileT& t, Job j, WaveAcc<D>& acc) {
+    auto consume_job = [&](TileT& t, const Job& j, WaveAcc<D>& acc) {
       const int tt0 = (wave + j.kk * NW) * kTile;
-      int t1 = tt0 + kTile;
-#pragma unroll
-      for (int i = 0; i < S; ++i)
-        if (j.i == i) t1 = (int)it.ctx[i];
+      const int t1 = tt0 + j.ntok;
       const bool on = lane_live && (j.i < 0 || ci == j.i);
-      if (tt0 + kTile > t1)
-        consume_tile<QT, CT, D, BS, false, true, true>(p, t, tt0, t1, lane_ctx, g, col, qa, qb, slope, acc, on);
+      // Columns that take no part in a job get p = 0, and 0 * inf is NaN:
+      // such jobs check V for non-finite values (consume_tile); a shared
+      // job of an item whose sequences are all live has every column on.
+      const bool partial = j.i >= 0 || !all_live;
+      if (j.ntok < kTile)
+        consume_tile<QT, CT, D, BS, false, true, true>(p, t, tt0, t1, lane_ctx, g, col, qa, qb, slope, acc, on, partial);
       else
-        consume_tile<QT, CT, D, BS, false, false, true>(p, t, tt0, t1, lane_ctx, g, col, qa, qb, slope, acc, on);
+        consume_tile<QT, CT, D, BS, false, false, true>(p, t, tt0, t1, lane_ctx, g, col, qa, qb, slope, acc, on,
+                                                        partial);
     };
 
+    // Ring of NB tile buffers: the loads of the next NB - 1 jobs are in
+    // flight while a job is consumed.  jb[b] is the job whose tile sits in
+    // t[b] (kk < 0: none, past the end of the list).
     WaveAcc<D> acc;
     acc.init();
-    Job cur = job_at(0);
-    if (cur.kk >= 0) {
-      TileT ta, tb;
-      load_job(ta, cur);
-      while (true) {
-        Job nx = next_job(cur);
-        if (nx.kk >= 0) load_job(tb, nx);
-        __builtin_amdgcn_s_waitcnt(kWaitAhead);
-        consume_job(ta, cur, acc);
-        if (nx.kk < 0) break;
-        cur = nx;
-        nx = next_job(cur);
-        if (nx.kk >= 0) load_job(ta, nx);
-        __builtin_amdgcn_s_waitcnt(kWaitAhead);
-        consume_job(tb, cur, acc);
-        if (nx.kk < 0) break;
-        cur = nx;
+    // The LDS entry of the job after the next one to load is read an
+    // iteration early, so its latency stays off the path to the next load.
+    if (njobs > 0) {
+      TileT t[NB];
+      Job jb[NB];
+#pragma unroll
+      for (int b = 0; b < NB - 1; ++b) {
+        jb[b] = job_of(b, entry_at(b));
+        if (jb[b].kk >= 0) load_job(t[b], jb[b]);
+      }
+      int4 ahead = entry_at(NB - 1);
+      int j = 0;
+      bool more = true;
+      while (more) {
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          const int sl = (b + NB - 1) % NB;
+          jb[sl] = job_of(j + NB - 1, ahead);
+          ahead = entry_at(j + NB);
+          if (jb[sl].kk >= 0) load_job(t[sl], jb[sl]);
+          __builtin_amdgcn_s_waitcnt(kWaitAhead);
+          consume_job(t[b], jb[b], acc);
+          ++j;
+          if (j >= njobs) {
+            more = false;
+            break;
+          }
+        }
       }
     }
-    merge_store_waves<QT, D, NW>(p, acc, s_red[buf], s_m[buf], s_l[buf], wave, lane, g, col,
+    // One merge buffer: every wavefront has read it (merge_store_waves)
+    // before any writes it for the next item.
+    merge_store_waves<QT, D, NW>(p, acc, s_red, s_m, s_l, wave, lane, g, col,
                                  (int64_t)lane_seq * p.num_heads + it.kvh * grp + hc, col_used && lane_seq >= 0);
-    buf ^= 1;
+    __syncthreads();
   }
 }
 
@@ -1961,7 +2093,10 @@ __global__ __launch_bounds__(64 * kMergeWaves) void paged_decode_reduce_kernel(D
   using QS = typename Elem<QT>::storage;
   constexpr int NW = kMergeWaves;
   constexpr int NDL = (D + 63) / 64;  // dimensions per lane
-  constexpr int U = 16;
+  // Partitions per wavefront and step: 256 per step in all, one step for
+  // the 512-token partitions of a 128K context, while the registers allow
+  // (head sizes up to 128).
+  constexpr int U = D <= 128 ? PKV_MERGE_U : 16;
   __shared__ float s_acc[NW][NDL * 64];
   __shared__ float s_m[NW];
   __shared__ float s_s[NW];
@@ -2094,21 +2229,23 @@ static hipError_t launch_grouped(const DecodeParams& p, hipStream_t stream, bool
   *launched = false;
   constexpr int S = kGroupSeqs;
   if (p.slices != 1 || p.group * S > 16 || p.max_seq_len > kGroupMaxSeq) return hipSuccess;
-  constexpr int NT = 64 * Persist<D>::kWaves;
+  constexpr int NW = PKV_GROUP_WAVES, NB = PKV_GROUP_NBUF;
+  constexpr int NT = 64 * NW;
   static int per_cu = -1;
   if (per_cu < 0) {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, paged_decode_group_kernel<QT, CT, D, BS, S>, NT, 0) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, paged_decode_group_kernel<QT, CT, D, BS, S, NW, NB>, NT, 0) !=
             hipSuccess ||
         n <= 0)
       n = 1;
     per_cu = n;
   }
   const int64_t items = (int64_t)((p.num_seqs + S - 1) / S) * p.num_kv_heads;
-  const int64_t grid = (int64_t)device_cus() * per_cu;
+  const int64_t grid = (int64_t)device_cus() * std::min(per_cu, PKV_GROUP_PER_CU);
   if (grid <= 0 || items < 2 * grid) return hipSuccess;
   *launched = true;
-  hipLaunchKernelGGL((paged_decode_group_kernel<QT, CT, D, BS, S>), dim3((unsigned)grid), dim3(NT), 0, stream, p);
+  hipLaunchKernelGGL((paged_decode_group_kernel<QT, CT, D, BS, S, NW, NB>), dim3((unsigned)grid), dim3(NT), 0, stream,
+                     p);
   return hipGetLastError();
 }
 
@@ -2134,13 +2271,13 @@ static hipError_t launch_persistent(const DecodeParams& p, hipStream_t stream, b
       n = 1;
     per_cu = n;
   }
-  // Whole (sequence, unit) items balance well once there are at least two
-  // per resident workgroup; fewer, longer items go to the partition path.
-  // The grid never exceeds what is resident at once, which the snake
-  // schedule assumes for its balance (not for correctness).
+  // Whole (sequence, unit) items, from one per resident workgroup; fewer,
+  // longer items go to the partition path.  The grid never exceeds what is
+  // resident at once, which the snake schedule assumes for its balance (not
+  // for correctness).
   const int64_t items = (int64_t)p.num_seqs * p.units;
   const int64_t grid = (int64_t)device_cus() * per_cu;
-  if (grid <= 0 || items < 2 * grid) return hipSuccess;
+  if (grid <= 0 || 4 * items < PKV_PERSIST_MIN4 * grid) return hipSuccess;
   *launched = true;
   hipLaunchKernelGGL((paged_decode_persist_kernel<QT, CT, D, BS>), dim3((unsigned)grid), dim3(NT), 0, stream, p);
   return hipGetLastError();
@@ -2152,8 +2289,16 @@ static hipError_t launch_one(const DecodeParams& p, hipStream_t stream) {
   const hipError_t pe = launch_persistent<QT, CT, D, BS>(p, stream, &launched);
   if (launched || pe != hipSuccess) return pe;
   const int64_t nwg = (int64_t)p.max_parts * p.num_seqs * p.units;
-  hipLaunchKernelGGL((paged_decode_part_kernel<QT, CT, D, BS, kPartWaves>), dim3((unsigned)nwg), dim3(64 * kPartWaves),
-                     0, stream, p);
+  // A grid of at most one workgroup per CU (one long sequence) gets eight
+  // wavefronts per workgroup, so each wavefront's chain of tiles is half as
+  // long; larger grids keep four, which leaves room for several workgroups
+  // per CU.
+  if (D <= 128 && nwg <= (int64_t)device_cus() * PKV_PART_SMALL_GRID)
+    hipLaunchKernelGGL((paged_decode_part_kernel<QT, CT, D, BS, 2 * kPartWaves>), dim3((unsigned)nwg),
+                       dim3(128 * kPartWaves), 0, stream, p);
+  else
+    hipLaunchKernelGGL((paged_decode_part_kernel<QT, CT, D, BS, kPartWaves>), dim3((unsigned)nwg), dim3(64 * kPartWaves),
+                       0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.max_parts == 1) return e;
   const int64_t rows = (int64_t)p.num_seqs * p.num_heads;
