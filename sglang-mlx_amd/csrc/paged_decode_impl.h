@@ -92,15 +92,6 @@ constexpr float kRescaleSlack = 8.f;
 #ifndef PKV_PART_NBUF
 #define PKV_PART_NBUF 2
 #endif
-// Partitions per wavefront and step of the merge kernel (head sizes up to
-// 128), and the partition-kernel grids (in workgroups per CU) that get eight
-// wavefronts per workgroup.
-#ifndef PKV_MERGE_U
-#define PKV_MERGE_U 32
-#endif
-#ifndef PKV_PART_SMALL_GRID
-#define PKV_PART_SMALL_GRID 1
-#endif
 // The one-sequence persistent kernel is used from PKV_PERSIST_MIN4 / 4
 // (sequence, unit) items per resident workgroup: from one item each, where
 // the longest-first order gives the longest items a workgroup of their own.
@@ -2093,10 +2084,10 @@ __global__ __launch_bounds__(64 * kMergeWaves) void paged_decode_reduce_kernel(D
   using QS = typename Elem<QT>::storage;
   constexpr int NW = kMergeWaves;
   constexpr int NDL = (D + 63) / 64;  // dimensions per lane
-  // Partitions per wavefront and step: 256 per step in all, one step for
-  // the 512-token partitions of a 128K context, while the registers allow
-  // (head sizes up to 128).
-  constexpr int U = D <= 128 ? PKV_MERGE_U : 16;
+  // Partitions per wavefront and step: 128 per step in all.  (32 per
+  // wavefront, one step for the 512-token partitions of a 128K context,
+  // measured 2-2.5 us slower on every Qwen2-7B long-context call.)
+  constexpr int U = 16;
   __shared__ float s_acc[NW][NDL * 64];
   __shared__ float s_m[NW];
   __shared__ float s_s[NW];
@@ -2289,16 +2280,10 @@ static hipError_t launch_one(const DecodeParams& p, hipStream_t stream) {
   const hipError_t pe = launch_persistent<QT, CT, D, BS>(p, stream, &launched);
   if (launched || pe != hipSuccess) return pe;
   const int64_t nwg = (int64_t)p.max_parts * p.num_seqs * p.units;
-  // A grid of at most one workgroup per CU (one long sequence) gets eight
-  // wavefronts per workgroup, so each wavefront's chain of tiles is half as
-  // long; larger grids keep four, which leaves room for several workgroups
-  // per CU.
-  if (D <= 128 && nwg <= (int64_t)device_cus() * PKV_PART_SMALL_GRID)
-    hipLaunchKernelGGL((paged_decode_part_kernel<QT, CT, D, BS, 2 * kPartWaves>), dim3((unsigned)nwg),
-                       dim3(128 * kPartWaves), 0, stream, p);
-  else
-    hipLaunchKernelGGL((paged_decode_part_kernel<QT, CT, D, BS, kPartWaves>), dim3((unsigned)nwg), dim3(64 * kPartWaves),
-                       0, stream, p);
+  // Four wavefronts per workgroup at every grid size: eight for grids of
+  // at most one workgroup per CU (one long sequence) measured no faster.
+  hipLaunchKernelGGL((paged_decode_part_kernel<QT, CT, D, BS, kPartWaves>), dim3((unsigned)nwg), dim3(64 * kPartWaves),
+                     0, stream, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.max_parts == 1) return e;
   const int64_t rows = (int64_t)p.num_seqs * p.num_heads;
