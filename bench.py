@@ -79,6 +79,9 @@ def parse_args():
     ap.add_argument("--no-rows", action="store_true", help="skip the token-row (MHATokenPool) decode measurement")
     ap.add_argument("--no-fp8", action="store_true", help="skip the FP8-cache decode measurement")
     ap.add_argument("--no-sweep", action="store_true", help="skip the batch-size sweep of the decode layer")
+    ap.add_argument("--lib", help="load libpagedkv_gfx950.so from this path instead of the package's (a build of the "
+                                  "same sources with other compile-time settings, e.g. make EXTRA_HIPFLAGS=... "
+                                  "OUTDIR=...), for A/B profiles")
     ap.add_argument("--only", choices=["decode", "append", "copy", "splitk", "radix", "radix_fp8", "rows", "fp8", "sweep"],
                     help="run one leg and print its own short JSON line (for counter collection under "
                          "rocprofv3 --pmc): the decode layer, the token-major append, or a plain 1 GiB device "
@@ -210,18 +213,24 @@ def graph_launch_ms(fn, launches: int, replays: int = 5):
 
 
 def read_traffic(name: str):
-    """HBM bytes per launch from a committed rocprofv3 counter summary
-    (profiles/<name>: a line 'traffic_bytes_per_launch: <int>'), else None."""
+    """(HBM bytes per launch, kernel average in us) from a committed
+    rocprofv3 counter summary (profiles/<name>: lines
+    'traffic_bytes_per_launch: <int>' and 'kernel_avg_us: <float>'), else
+    (None, None)."""
     path = os.path.join(ROOT, "profiles", name)
+    traffic = avg = None
     try:
         with open(path) as f:
             for line in f:
                 m = re.match(r"\s*traffic_bytes_per_launch:\s*([0-9.eE+]+)", line)
                 if m:
-                    return int(float(m.group(1)))
+                    traffic = int(float(m.group(1)))
+                m = re.match(r"\s*kernel_avg_us:\s*([0-9.eE+]+)", line)
+                if m:
+                    avg = float(m.group(1))
     except OSError:
         pass
-    return None
+    return traffic, avg
 
 
 # ---------------------------------------------------------------------------
@@ -571,6 +580,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
         sys.exit(1)
+    if args.lib:
+        from sglang_mlx_amd import _lib
+        _lib.LIB_PATH = os.path.abspath(args.lib)
     from sglang_mlx_amd import kernels
 
     dev = torch.device("cuda:0")
@@ -581,6 +593,19 @@ def main():
     res = bench_decode(args, dev, kernels)
     inp = res["inp"]
     B = inp["B"]
+    # The counter summary's traffic holds for the build it was measured on:
+    # it is marked stale when this run's mean launch time differs from the
+    # kernel average recorded with it by more than 5%.
+    traffic, traffic_avg_us = read_traffic("paged_decode_llama3_8b_traffic.txt")
+    mean_us = res["mean_ms"] * 1e3
+    if traffic is None:
+        traffic_note = "no counter summary"
+    elif traffic_avg_us is None or abs(mean_us - traffic_avg_us) > 0.05 * traffic_avg_us:
+        traffic_note = (f"STALE: profiles/paged_decode_llama3_8b_traffic.txt was measured at a kernel average of "
+                        f"{traffic_avg_us} us, this run's mean launch is {mean_us:.2f} us")
+    else:
+        traffic_note = (f"profiles/paged_decode_llama3_8b_traffic.txt (rocprofv3 FETCH_SIZE + WRITE_SIZE, calibrated; "
+                        f"kernel average there {traffic_avg_us} us, here {mean_us:.2f} us)")
     us = res["ms_step"] * 1e3
     value = res["nbytes"] / (res["ms_step"] * 1e-3) / 1e9
     line = {
@@ -611,7 +636,8 @@ def main():
             "peak": PEAK_GBS,
             "unit": "GB/s",
             "frac": round(res["achieved"] / PEAK_GBS, 4),
-            "traffic": read_traffic("paged_decode_llama3_8b_traffic.txt"),
+            "traffic": traffic,
+            "traffic_source": traffic_note,
             "kernel": DECODE_KERNEL,
             "bytes_per_launch": res["nbytes"],
             "mean_launch_us": round(res["mean_ms"] * 1e3, 2),

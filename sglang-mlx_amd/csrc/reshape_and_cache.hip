@@ -122,42 +122,112 @@ __global__ __launch_bounds__(256) void rac_token_major_kernel(RacParams p) {
 // written once and nothing in this launch reads it back.  (Inactive lanes
 // take zeros through a conditional expression; guarding the loads with an
 // if-statement instead measured ~15% slower at the same instruction count.)
+// The source rows are loaded with the nontemporal policy when no conversion
+// is needed: each is read once.
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
+// Measured at 4096 tokens x 8 heads x D 128, bf16, 65,536 slots (median of
+// interleaved runs, one process per variant): one token per wavefront, four
+// wavefronts per workgroup, default-policy source loads 6.64 us; with
+// nontemporal source loads (each source row is read once) 6.29 us; two or
+// eight wavefronts per workgroup 6.62 / 6.60 us; two tokens per wavefront
+// 6.85 us; one wavefront per (token, head) 9.68 us.
+#ifndef PKV_RAC_TPW
+#define PKV_RAC_TPW 1  // tokens per wavefront
+#endif
+#ifndef PKV_RAC_WAVES
+#define PKV_RAC_WAVES 4  // wavefronts per workgroup
+#endif
+#ifndef PKV_RAC_NTLOAD
+#define PKV_RAC_NTLOAD 1  // nontemporal source loads
+#endif
+#ifndef PKV_RAC_PER_HEAD
+#define PKV_RAC_PER_HEAD 0  // one wavefront per (token, head)
+#endif
+
+template <class KT, class CT>
+__device__ __forceinline__ uint4 load_src16(const typename Elem<KT>::storage* src) {
+  if constexpr (PKV_RAC_NTLOAD && std::is_same<KT, CT>::value) {
+    return __builtin_bit_cast(uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(src)));
+  } else {
+    return load_vec16<KT, CT>(src);
+  }
+}
+
 template <class KT, class CT, int NV>
-__global__ __launch_bounds__(256) void rac_token_major_wave_kernel(RacParams p) {
+__global__ __launch_bounds__(64 * PKV_RAC_WAVES) void rac_token_major_wave_kernel(RacParams p) {
   using KS = typename Elem<KT>::storage;
   using CS = typename Elem<CT>::storage;
   constexpr int VE = 16 / Elem<CT>::kBytes;  // elements per 16-byte cache vector
+  constexpr int TPW = PKV_RAC_TPW;
   const int lane = threadIdx.x & 63;
-  const int tok = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
-  // Wavefronts past the last token stay for the barrier and move nothing.
-  const bool live = tok < p.num_tokens;
+  const int tok0 = ((int)blockIdx.x * PKV_RAC_WAVES + (int)(threadIdx.x >> 6)) * TPW;
   const int row = p.num_heads * p.head_size;
   const int nvec = row / VE;  // 64 * (NV/2) < nvec <= 64 * NV
-  const int32_t slot = live ? p.slot_mapping[tok] : -1;
-  const KS* ksrc = static_cast<const KS*>(p.key) + (int64_t)tok * p.key_stride;
-  const KS* vsrc = static_cast<const KS*>(p.value) + (int64_t)tok * p.value_stride;
-  uint4 kx[NV], vx[NV];
+  uint4 kx[TPW][NV], vx[TPW][NV];
+  int32_t slot[TPW];
 #pragma unroll
-  for (int c = 0; c < NV; ++c) {
-    const int i = 64 * c + lane;
-    const bool ok = live && i < nvec;
-    kx[c] = ok ? load_vec16<KT, CT>(ksrc + i * VE) : make_uint4(0, 0, 0, 0);
-    vx[c] = ok ? load_vec16<KT, CT>(vsrc + i * VE) : make_uint4(0, 0, 0, 0);
-  }
-  __syncthreads();
-  if (slot >= 0 && (int64_t)slot < p.num_slots) {
-    CS* kdst = static_cast<CS*>(p.key_cache) + (int64_t)slot * row;
-    CS* vdst = static_cast<CS*>(p.value_cache) + (int64_t)slot * row;
+  for (int u = 0; u < TPW; ++u) {
+    const int tok = tok0 + u;
+    // Wavefronts past the last token stay for the barrier and move nothing.
+    const bool live = tok < p.num_tokens;
+    slot[u] = live ? p.slot_mapping[tok] : -1;
+    const KS* ksrc = static_cast<const KS*>(p.key) + (int64_t)tok * p.key_stride;
+    const KS* vsrc = static_cast<const KS*>(p.value) + (int64_t)tok * p.value_stride;
 #pragma unroll
     for (int c = 0; c < NV; ++c) {
       const int i = 64 * c + lane;
-      if (i < nvec) {
-        __builtin_nontemporal_store(__builtin_bit_cast(u32x4_t, kx[c]), reinterpret_cast<u32x4_t*>(kdst + i * VE));
-        __builtin_nontemporal_store(__builtin_bit_cast(u32x4_t, vx[c]), reinterpret_cast<u32x4_t*>(vdst + i * VE));
+      const bool ok = live && i < nvec;
+      kx[u][c] = ok ? load_src16<KT, CT>(ksrc + i * VE) : make_uint4(0, 0, 0, 0);
+      vx[u][c] = ok ? load_src16<KT, CT>(vsrc + i * VE) : make_uint4(0, 0, 0, 0);
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < TPW; ++u) {
+    if (slot[u] >= 0 && (int64_t)slot[u] < p.num_slots) {
+      CS* kdst = static_cast<CS*>(p.key_cache) + (int64_t)slot[u] * row;
+      CS* vdst = static_cast<CS*>(p.value_cache) + (int64_t)slot[u] * row;
+#pragma unroll
+      for (int c = 0; c < NV; ++c) {
+        const int i = 64 * c + lane;
+        if (i < nvec) {
+          __builtin_nontemporal_store(__builtin_bit_cast(u32x4_t, kx[u][c]), reinterpret_cast<u32x4_t*>(kdst + i * VE));
+          __builtin_nontemporal_store(__builtin_bit_cast(u32x4_t, vx[u][c]), reinterpret_cast<u32x4_t*>(vdst + i * VE));
+        }
       }
     }
+  }
+}
+
+// ---- token-major layout: one wavefront per (token, head) ----------------------------
+// The north star's decomposition, kept for comparison with the one above:
+// lanes 0 .. D/VE-1 move the head's K vectors and the next D/VE lanes its V
+// vectors (32 of 64 lanes at D = 128 with 16-bit caches), same
+// load / barrier / nontemporal-store phases.
+template <class KT, class CT>
+__global__ __launch_bounds__(256) void rac_token_major_head_kernel(RacParams p) {
+  using KS = typename Elem<KT>::storage;
+  using CS = typename Elem<CT>::storage;
+  constexpr int VE = 16 / Elem<CT>::kBytes;
+  const int lane = threadIdx.x & 63;
+  const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const bool live = wid < p.num_tokens * p.num_heads;
+  const int64_t tok = live ? wid / p.num_heads : 0;
+  const int head = live ? (int)(wid - tok * p.num_heads) : 0;
+  const int hv = p.head_size / VE;  // vectors per head
+  const bool is_v = lane >= hv;
+  const int i = is_v ? lane - hv : lane;
+  const bool ok = live && lane < 2 * hv;
+  const int32_t slot = live ? p.slot_mapping[tok] : -1;
+  const KS* src = static_cast<const KS*>(is_v ? p.value : p.key) + tok * (is_v ? p.value_stride : p.key_stride) +
+                  (int64_t)head * p.head_size + i * VE;
+  const uint4 x = ok ? load_src16<KT, CT>(src) : make_uint4(0, 0, 0, 0);
+  __syncthreads();
+  if (ok && slot >= 0 && (int64_t)slot < p.num_slots) {
+    CS* dst = static_cast<CS*>(is_v ? p.value_cache : p.key_cache) +
+              ((int64_t)slot * p.num_heads + head) * p.head_size + i * VE;
+    __builtin_nontemporal_store(__builtin_bit_cast(u32x4_t, x), reinterpret_cast<u32x4_t*>(dst));
   }
 }
 
@@ -277,17 +347,23 @@ static hipError_t launch_rac_typed(const RacParams& p, bool aligned, hipStream_t
     int threads = vec ? 2 * (row / VE) : 2 * row;
     threads = threads >= 256 ? 256 : ((threads + 63) / 64) * 64;
     const dim3 grid((unsigned)p.num_tokens);
-    // The one-wavefront-per-token kernels index tokens with 32-bit ints.
-    const int nvec = (vec && p.num_tokens <= INT32_MAX - 3) ? row / VE : 0;
-    const dim3 wgrid((unsigned)((p.num_tokens + 3) / 4));
-    if (vec && nvec > 64 && nvec <= 128)
-      hipLaunchKernelGGL((rac_token_major_wave_kernel<KT, CT, 2>), wgrid, dim3(256), 0, stream, p);
+    // The one-wavefront-per-token kernels index tokens with 32-bit ints
+    // (a workgroup covers at most 64 tokens).
+    const int nvec = (vec && p.num_tokens <= INT32_MAX - 64) ? row / VE : 0;
+    const int64_t per_wg = (int64_t)PKV_RAC_WAVES * PKV_RAC_TPW;
+    const dim3 wgrid((unsigned)((p.num_tokens + per_wg - 1) / per_wg));
+    if (PKV_RAC_PER_HEAD && vec && p.head_size / VE <= 32) {
+      const int64_t waves = p.num_tokens * p.num_heads;
+      hipLaunchKernelGGL((rac_token_major_head_kernel<KT, CT>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream,
+                         p);
+    } else if (vec && nvec > 64 && nvec <= 128)
+      hipLaunchKernelGGL((rac_token_major_wave_kernel<KT, CT, 2>), wgrid, dim3(64 * PKV_RAC_WAVES), 0, stream, p);
     else if (vec && nvec > 128 && nvec <= 256)
-      hipLaunchKernelGGL((rac_token_major_wave_kernel<KT, CT, 4>), wgrid, dim3(256), 0, stream, p);
+      hipLaunchKernelGGL((rac_token_major_wave_kernel<KT, CT, 4>), wgrid, dim3(64 * PKV_RAC_WAVES), 0, stream, p);
     else if (vec && nvec > 256 && nvec <= 512)
-      hipLaunchKernelGGL((rac_token_major_wave_kernel<KT, CT, 8>), wgrid, dim3(256), 0, stream, p);
+      hipLaunchKernelGGL((rac_token_major_wave_kernel<KT, CT, 8>), wgrid, dim3(64 * PKV_RAC_WAVES), 0, stream, p);
     else if (vec && nvec > 512 && nvec <= 1024)
-      hipLaunchKernelGGL((rac_token_major_wave_kernel<KT, CT, 16>), wgrid, dim3(256), 0, stream, p);
+      hipLaunchKernelGGL((rac_token_major_wave_kernel<KT, CT, 16>), wgrid, dim3(64 * PKV_RAC_WAVES), 0, stream, p);
     else if (vec)
       hipLaunchKernelGGL((rac_token_major_kernel<KT, CT, VE, true>), grid, dim3(threads), 0, stream, p);
     else
