@@ -67,7 +67,10 @@ __device__ __forceinline__ float wave_sum(float x) {
 // round-to-nearest-even conversions; probabilities are never NaN).
 template <class CT> __device__ __forceinline__ uint32_t pack_p(float a, float b);
 template <> __device__ __forceinline__ uint32_t pack_p<BF16>(float a, float b) {
-  return pack2(__builtin_bit_cast(uint16_t, (__bf16)a), __builtin_bit_cast(uint16_t, (__bf16)b));
+  // One v_cvt_pk_bf16_f32 (round to nearest even, as the scalar conversion).
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
 }
 template <> __device__ __forceinline__ uint32_t pack_p<F16>(float a, float b) {
   return pack2(__builtin_bit_cast(uint16_t, (_Float16)a), __builtin_bit_cast(uint16_t, (_Float16)b));
@@ -82,6 +85,9 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 // below 2^8, and the rescale of the accumulators is skipped for almost every
 // tile.  Any reference maximum gives the same normalised result.
 constexpr float kRescaleSlack = 8.f;
+#ifndef PKV_INPLACE_RESCALE
+#define PKV_INPLACE_RESCALE 1
+#endif
 
 #ifndef PKV_NBUF
 #define PKV_NBUF 4
@@ -921,8 +927,18 @@ __device__ __forceinline__ void softmax_tile(const DecodeParams& p, f32x4 sacc, 
     const float m_new = fmaxf(acc.m_run, mt);
     const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(acc.m_run - m_new);
     acc.l_run *= alpha;
+#if PKV_INPLACE_RESCALE
+    // In place (each register multiplied where it lives): as a plain
+    // product the compiler copied all DT x 4 accumulators on the path that
+    // skips the rescale, every tile.
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) asm("v_mul_f32 %0, %0, %1" : "+v"(acc.o[dt][r]) : "v"(alpha));
+#else
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) acc.o[dt] *= alpha;
+#endif
     acc.m_run = m_new;
   }
   const float m_use = acc.m_run == -INFINITY ? 0.f : acc.m_run;
@@ -1142,8 +1158,8 @@ __device__ __forceinline__ void stream_tiles(const DecodeParams& p, const typena
                                              int first, int g, int col, const uint4 (&qa)[Tile<D>::KSTEPS],
                                              const uint4 (&qb)[std::is_same<QT, F32>::value ? Tile<D>::KSTEPS : 1],
                                              float slope, WaveAcc<D>& acc) {
-  constexpr int KSTEPS = Tile<D>::KSTEPS;
-  constexpr int DT = Tile<D>::DT;
+  [[maybe_unused]] constexpr int KSTEPS = Tile<D>::KSTEPS;
+  [[maybe_unused]] constexpr int DT = Tile<D>::DT;
   constexpr int PT = WaveBlocks<BS, MAXT>::PER_TILE;
   constexpr bool F8 = std::is_same<CT, FP8>::value;
   constexpr bool F32C = std::is_same<CT, F32>::value;
@@ -1783,6 +1799,12 @@ template <int S> struct GroupItem {
 #ifndef PKV_GROUP_PER_CU
 #define PKV_GROUP_PER_CU 1
 #endif
+// Cache policy of the grouped kernel's tile loads: 0 = nontemporal for
+// private tiles only, 1 = nontemporal for all, 2 = default for all.
+#ifndef PKV_GROUP_CPOL
+#define PKV_GROUP_CPOL 0
+#endif
+
 
 template <class QT, class CT, int D, int BS, int S, int NW, int NB>
 __global__ __launch_bounds__(64 * NW) void paged_decode_group_kernel(DecodeParams p) {
@@ -1811,7 +1833,13 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_group_kernel(DecodeParam
   __shared__ float s_l[NW][16];
   __shared__ __align__(16) uint32_t s_ctx[kPersistMaxOrder];
   __shared__ int32_t s_order[kPersistMaxOrder];
-  __shared__ int4 s_jobs[NW][MAXT * S];  // per wavefront: the item's job list
+  // The item's job list, dealt to the wavefronts round-robin.  One-block
+  // tiles (PT == 1) take (block, meta); two-block tiles (block, block, meta,
+  // unused).  s_cnt: each wavefront's share of the list while it is built.
+  using JobEntry = std::conditional_t<PT == 1, int2, int4>;
+  __shared__ JobEntry s_jobs[NW * MAXT * S];
+  __shared__ int s_cnt[NW];
+  static_assert(NW * MAXT <= 1024 && S <= 14, "job meta holds tile < 1024 and slot + 1 < 15");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1908,32 +1936,38 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_group_kernel(DecodeParam
     const CS* kbase = static_cast<const CS*>(p.k_cache) + (int64_t)it.kvh * p.k_head_stride;
     const CS* vbase = static_cast<const CS*>(p.v_cache) + (int64_t)it.kvh * p.v_head_stride;
 
-    // Job list of this wavefront, built once per item: lane n describes
-    // the wavefront's tile kk(n) -- taken from both ends in turn (0, K-1,
-    // 1, K-2, ...), so that the shared prefix alternates with the private
-    // tails and L2-served and HBM-served loads overlap.  A tile is
+    // Job list of the item, built once: lane n of wavefront w describes
+    // tile w + NW kk(n), kk taken from both ends in turn (0, K-1, 1, K-2,
+    // ...), so that the shared prefix alternates with the private tails and
+    // L2-served and HBM-served loads overlap.  A tile is
     //   * shared: every live sequence maps it to the same block(s) and holds
     //     all 16 of its tokens -- one job that feeds every column, so a
     //     radix-shared prefix is read once per S sequences;
     //   * otherwise one job per sequence that reaches it, with only that
     //     sequence's columns active.
-    // A wave prefix sum of the lanes' job counts places each lane's jobs in
-    // the wavefront's LDS list: (block of tokens 0-7, block of tokens 8-15,
-    // kk | (sequence slot + 1, 0 = shared) << 8 | valid tokens << 16).
-    const int K = maxnt > wave ? (maxnt - 1 - wave) / NW + 1 : 0;  // tiles of this wavefront
-    int njobs = 0;
+    // A wave prefix sum of the lanes' job counts, offset by the earlier
+    // wavefronts' counts, places each lane's jobs in the item's LDS list:
+    // (block of tokens 0-7, block of tokens 8-15, tile | (sequence slot + 1,
+    // 0 = shared) << 10 | valid tokens << 16).  Wavefront w then runs jobs
+    // w, w + NW, ...: the item's jobs split within one per wavefront, where
+    // whole tiles per wavefront left the first wavefronts up to one job per
+    // sequence ahead (every sequence's last tile falls to them), and the
+    // item's merge waits for the last.
+    const int K = maxnt > wave ? (maxnt - 1 - wave) / NW + 1 : 0;  // tiles this wavefront lists
+    int wjobs = 0, incl = 0, cnt = 0;
+    int kk = 0, fb0 = 0, fb1 = 0;
+    bool shared = false;
+    int b0[S], b1[S];
     if (K > 0) {
       const bool has = lane < K;
-      const int kk = (lane & 1) ? K - 1 - (lane >> 1) : (lane >> 1);
+      kk = (lane & 1) ? K - 1 - (lane >> 1) : (lane >> 1);
       const int tt0 = (wave + kk * NW) * kTile;
-      int b0[S], b1[S];
 #pragma unroll
       for (int i = 0; i < S; ++i) {
         b0[i] = blk[i].fetch(kk * PT);
         b1[i] = PT == 2 ? blk[i].fetch(kk * PT + 1) : b0[i];
       }
-      bool shared = tt0 + kTile <= (int)minctx;
-      int fb0 = 0, fb1 = 0;
+      shared = tt0 + kTile <= (int)minctx;
 #pragma unroll
       for (int i = 0; i < S; ++i) {
         if (it.ctx[i] == 0) continue;
@@ -1944,7 +1978,6 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_group_kernel(DecodeParam
           shared = shared && b0[i] == fb0 && b1[i] == fb1;
         }
       }
-      int cnt = 0;
       if (has) {
         if (shared) {
           cnt = 1;
@@ -1953,53 +1986,88 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_group_kernel(DecodeParam
           for (int i = 0; i < S; ++i) cnt += tt0 < (int)it.ctx[i];
         }
       }
-      int incl = cnt;  // inclusive prefix sum over the lanes
+      incl = cnt;  // inclusive prefix sum over the lanes
 #pragma unroll
       for (int o = 1; o < 64; o <<= 1) {
         const int y = __shfl_up(incl, o);
         incl += lane >= o ? y : 0;
       }
-      njobs = __builtin_amdgcn_readlane(incl, 63);
-      int4* list = s_jobs[wave];
-      int at = incl - cnt;
-      if (has) {
-        if (shared) {
-          list[at] = make_int4(fb0, fb1, kk | (kTile << 16), 0);
-        } else {
+      wjobs = __builtin_amdgcn_readlane(incl, 63);
+    }
+    if (lane == 0) s_cnt[wave] = wjobs;
+    __syncthreads();
+    int base = 0, item_jobs = 0;
 #pragma unroll
-          for (int i = 0; i < S; ++i) {
-            if (tt0 < (int)it.ctx[i]) {
-              const int ntok = min(kTile, (int)it.ctx[i] - tt0);
-              list[at++] = make_int4(b0[i], b1[i], kk | ((i + 1) << 8) | (ntok << 16), 0);
-            }
+    for (int w = 0; w < NW; ++w) {
+      const int c = s_cnt[w];
+      base += w < wave ? c : 0;
+      item_jobs += c;
+    }
+    if (cnt > 0) {
+      auto entry = [](int blk0, int blk1, int meta) {
+        if constexpr (PT == 1)
+          return make_int2(blk0, meta);
+        else
+          return make_int4(blk0, blk1, meta, 0);
+      };
+      const int tile = wave + kk * NW;
+      const int tt0 = tile * kTile;
+      int at = base + incl - cnt;
+      if (shared) {
+        s_jobs[at] = entry(fb0, fb1, tile | (kTile << 16));
+      } else {
+#pragma unroll
+        for (int i = 0; i < S; ++i) {
+          if (tt0 < (int)it.ctx[i]) {
+            const int ntok = min(kTile, (int)it.ctx[i] - tt0);
+            s_jobs[at++] = entry(b0[i], b1[i], tile | ((i + 1) << 10) | (ntok << 16));
           }
         }
       }
     }
-    // The list is read back by every lane of the same wavefront only: the
-    // wavefront's LDS operations complete in order, and the barrier keeps
-    // the compiler from moving the reads above the writes.
-    __builtin_amdgcn_wave_barrier();
+    __syncthreads();
+    const int njobs = item_jobs > wave ? (item_jobs - 1 - wave) / NW + 1 : 0;  // this wavefront's jobs
     struct Job {
-      int b0, b1, kk, i, ntok;  // i = -1: shared; kk < 0: none
+      int b0, b1, tile, i, ntok;  // i = -1: shared
+      bool pad;                   // past the wavefront's last job (see load_job)
     };
-    // Entry j of the list as read from LDS (every lane reads the same
-    // entry), and as a wave-uniform job.
-    auto entry_at = [&](int j) -> int4 { return s_jobs[wave][j < njobs ? j : 0]; };
-    auto job_of = [&](int j, int4 e) -> Job {
-      if (j >= njobs) return Job{0, 0, -1, -1, 0};
-      const int meta = __builtin_amdgcn_readfirstlane(e.z);
-      return Job{__builtin_amdgcn_readfirstlane(e.x), PT == 2 ? __builtin_amdgcn_readfirstlane(e.y) : 0,
-                 meta & 0xff, ((meta >> 8) & 0xff) - 1, meta >> 16};
+    // The wavefront's job j (item list entry wave + NW j) as read from LDS
+    // (every lane reads the same entry), and as a wave-uniform job.  Past
+    // the wavefront's last job: the item's first job, as padding.
+    auto entry_at = [&](int j) -> JobEntry { return s_jobs[j < njobs ? wave + NW * j : 0]; };
+    auto job_of = [&](int j, JobEntry e) -> Job {
+      int b0, b1, meta;
+      if constexpr (PT == 1) {
+        b0 = e.x;
+        b1 = e.x;
+        meta = e.y;
+      } else {
+        b0 = e.x;
+        b1 = e.y;
+        meta = e.z;
+      }
+      meta = __builtin_amdgcn_readfirstlane(meta);
+      return Job{__builtin_amdgcn_readfirstlane(b0), PT == 2 ? __builtin_amdgcn_readfirstlane(b1) : 0, meta & 0x3ff,
+                 ((meta >> 10) & 0x3f) - 1, meta >> 16, j >= njobs};
     };
-    auto load_job = [&](TileT& t, const Job& j) {
-      const int b0 = j.b0, b1 = PT == 2 ? j.b1 : j.b0;
-      const int tt0 = (wave + j.kk * NW) * kTile;
-      // A private job's tile is read once (nt, as in stream_tiles); a shared
-      // tile keeps the default policy, as the other items of its KV head
-      // read it from L2.  Radix-shared B256 workload: 106.7 -> 103.7 us
-      // (same process; nt on every load: 109.8 against 109.2 us).
-      if (j.i >= 0) {
+    // Every pipeline step issues one job's loads, padding past the last job
+    // included, so that every step waits for the same count: a conditional
+    // load makes the compiler wait for all outstanding loads (vmcnt(0))
+    // before each tile is consumed, the next job's too, which left no load
+    // in flight during the MFMA work (the one-sequence kernel's tile stream
+    // pads the same way).  A padding load gets the zero-sized buffer
+    // resource of a masked block with blocks of 16 and more (it reads
+    // nothing); with smaller blocks it re-reads the item's first tile.
+    // NT: the job's loads use the nontemporal policy (a private tile, read
+    // once); shared tiles keep the default one, as the other items of their
+    // KV head read them from L2.
+    auto load_job = [&](TileT& t, const Job& j, auto NT) {
+      int b0 = j.b0, b1 = PT == 2 ? j.b1 : j.b0;
+      if constexpr (BS >= kTile) {
+        if (j.pad) b0 = b1 = -1;
+      }
+      const int tt0 = j.tile * kTile;
+      if constexpr (decltype(NT)::value) {
         if constexpr (F8)
           load_tile_fp8<D, BS, kStreamCpol>(t, kbase, vbase, p.k_block_stride, p.v_block_stride, b0, b1, tt0, g, col);
         else
@@ -2012,7 +2080,7 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_group_kernel(DecodeParam
       }
     };
     auto consume_job = [&](TileT& t, const Job& j, WaveAcc<D>& acc) {
-      const int tt0 = (wave + j.kk * NW) * kTile;
+      const int tt0 = j.tile * kTile;
       const int t1 = tt0 + j.ntok;
       const bool on = lane_live && (j.i < 0 || ci == j.i);
       // Columns that take no part in a job get p = 0, and 0 * inf is NaN:
@@ -2028,20 +2096,26 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_group_kernel(DecodeParam
 
     // Ring of NB tile buffers: the loads of the next NB - 1 jobs are in
     // flight while a job is consumed.  jb[b] is the job whose tile sits in
-    // t[b] (kk < 0: none, past the end of the list).
+    // t[b] (padding past the wavefront's last job).  The LDS entry of the
+    // job after the next one to load is read an iteration early, so its
+    // latency stays off the path to the next load.  (Two LDS slots per
+    // wavefront filled by buffer-to-LDS loads, for two jobs in flight during
+    // each consume, measured slower: 108.2 against 101.6 us on the
+    // radix-shared B256 workload.)
     WaveAcc<D> acc;
     acc.init();
-    // The LDS entry of the job after the next one to load is read an
-    // iteration early, so its latency stays off the path to the next load.
     if (njobs > 0) {
       TileT t[NB];
       Job jb[NB];
 #pragma unroll
       for (int b = 0; b < NB - 1; ++b) {
         jb[b] = job_of(b, entry_at(b));
-        if (jb[b].kk >= 0) load_job(t[b], jb[b]);
+        if (jb[b].i >= 0)
+          load_job(t[b], jb[b], std::true_type{});
+        else
+          load_job(t[b], jb[b], std::false_type{});
       }
-      int4 ahead = entry_at(NB - 1);
+      JobEntry ahead = entry_at(NB - 1);
       int j = 0;
       bool more = true;
       while (more) {
@@ -2050,9 +2124,18 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_group_kernel(DecodeParam
           const int sl = (b + NB - 1) % NB;
           jb[sl] = job_of(j + NB - 1, ahead);
           ahead = entry_at(j + NB);
-          if (jb[sl].kk >= 0) load_job(t[sl], jb[sl]);
-          __builtin_amdgcn_s_waitcnt(kWaitAhead);
-          consume_job(t[b], jb[b], acc);
+          // Each branch issues its loads, waits and consumes: with the
+          // loads alone in the branches the compiler saw a path with no loads
+          // and waited for all of them (vmcnt(0)) before every tile.
+          if (PKV_GROUP_CPOL == 1 || (PKV_GROUP_CPOL == 0 && jb[sl].i >= 0)) {
+            load_job(t[sl], jb[sl], std::true_type{});
+            __builtin_amdgcn_s_waitcnt(kWaitAhead);
+            consume_job(t[b], jb[b], acc);
+          } else {
+            load_job(t[sl], jb[sl], std::false_type{});
+            __builtin_amdgcn_s_waitcnt(kWaitAhead);
+            consume_job(t[b], jb[b], acc);
+          }
           ++j;
           if (j >= njobs) {
             more = false;
