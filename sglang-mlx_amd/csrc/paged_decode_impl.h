@@ -1610,43 +1610,68 @@ template <int D, bool ROWS = false, bool F8 = false> struct Persist {
   static constexpr int kMaxBuf = ROWS ? PKV_ROWS_NBUF : F8 ? PKV_FP8_NBUF : PKV_PAGED_NBUF;
 };
 
+// Rank of each of the first n entries of s_keys (distinct keys; the array
+// is padded to a multiple of 16 bytes with keys that never count) among all
+// of them, into s_order[rank] = index: DESC ranks larger keys first,
+// otherwise smaller ones.  tp = the threads that share one entry's count
+// (a power of two, at most 16), each counting a slice of the keys, read 16
+// bytes per LDS load (the same address in every lane of the slice group, a
+// broadcast); the partial counts meet through lane shuffles.  Every thread
+// of the workgroup calls it; it ends with a workgroup barrier.
+template <class K, bool DESC>
+__device__ __forceinline__ void rank_keys(const K* s_keys, int n, int32_t* s_order, int tid, int nt) {
+  constexpr int PER = 16 / sizeof(K);  // keys per 16-byte load
+  const int nv = (n + PER - 1) / PER;  // 16-byte loads that cover the keys
+  int tp = 1;
+  while (tp < 16 && tp * 2 * n <= nt) tp *= 2;
+  for (int base = 0; base < n * tp; base += nt) {
+    const int t = base + tid;
+    const int e = t / tp, part = t - e * tp;
+    int r = 0;
+    if (e < n) {
+      const K k = s_keys[e];
+      const int v0 = part * nv / tp, v1 = (part + 1) * nv / tp;
+#pragma unroll 4
+      for (int v = v0; v < v1; ++v) {
+        if constexpr (sizeof(K) == 4) {
+          const uint4 w = reinterpret_cast<const uint4*>(s_keys)[v];
+          r += DESC ? (w.x > k) + (w.y > k) + (w.z > k) + (w.w > k) : (w.x < k) + (w.y < k) + (w.z < k) + (w.w < k);
+        } else {
+          const ulonglong2 w = reinterpret_cast<const ulonglong2*>(s_keys)[v];
+          r += DESC ? (w.x > k) + (w.y > k) : (w.x < k) + (w.y < k);
+        }
+      }
+    }
+    for (int o = 1; o < tp; o <<= 1) r += __shfl_xor(r, o);
+    if (e < n && part == 0) s_order[r] = e;
+  }
+  __syncthreads();
+}
+
 // Longest-first rank of the sequences (ties by index) into s_order, when
 // there are at most kPersistMaxOrder of them (returns whether it did).
 // Empty and over-long contexts (zero rows) count as length 0.  Every thread
-// of the workgroup calls it.  s_ctx (16-byte aligned) is padded with zeros
-// to a multiple of 4 entries, which never count: a padding entry is not
-// longer than any context, and its index is past every real one.  The
-// count then reads four lengths per LDS load (the same address in every
-// lane, a broadcast) with several loads in flight, instead of one dependent
-// load per sequence: B loads per thread at up to 1024 sequences.
-__device__ __forceinline__ bool rank_sequences(const DecodeParams& p, uint32_t* s_ctx, int32_t* s_order, int tid,
+// of the workgroup calls it.  Each sequence's key is its length above its
+// inverted index, (len << 10) | (1023 - s), so that keys are distinct and
+// one comparison orders two sequences; the padding to a multiple of 4
+// entries holds 0, below every real key.
+static_assert(kPersistMaxOrder == 1024 && kPersistMaxSeq < (1 << 22), "rank keys are (length << 10) | index");
+__device__ __forceinline__ bool rank_sequences(const DecodeParams& p, uint32_t* s_key, int32_t* s_order, int tid,
                                                int nt) {
   const int B = p.num_seqs;
   if (B > kPersistMaxOrder) return false;
   const int B4 = (B + 3) & ~3;  // kPersistMaxOrder is a multiple of 4
   for (int s = tid; s < B4; s += nt) {
-    uint32_t c = 0;
+    uint32_t key = 0;
     if (s < B) {
-      c = (uint32_t)p.context_lens[s];
+      uint32_t c = (uint32_t)p.context_lens[s];
       c = c > (uint32_t)p.max_seq_len ? 0u : c;
+      key = (c << 10) | (uint32_t)(kPersistMaxOrder - 1 - s);
     }
-    s_ctx[s] = c;
+    s_key[s] = key;
   }
   __syncthreads();
-  for (int s = tid; s < B; s += nt) {
-    const uint32_t c = s_ctx[s];
-    int r = 0;
-#pragma unroll 4
-    for (int s2 = 0; s2 < B4; s2 += 4) {
-      const uint4 w = *reinterpret_cast<const uint4*>(s_ctx + s2);
-      r += (w.x > c) || (w.x == c && s2 < s);
-      r += (w.y > c) || (w.y == c && s2 + 1 < s);
-      r += (w.z > c) || (w.z == c && s2 + 2 < s);
-      r += (w.w > c) || (w.w == c && s2 + 3 < s);
-    }
-    s_order[r] = s;
-  }
-  __syncthreads();
+  rank_keys<uint32_t, true>(s_key, B, s_order, tid, nt);
   return true;
 }
 
