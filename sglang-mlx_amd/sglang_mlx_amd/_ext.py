@@ -245,7 +245,10 @@ def paged_attention_v2(query, key_cache, value_cache, block_tables, seq_lens, nu
                        v_scale=1.0):
     """Split-K paged decode: softmax per partition of ``partition_size``
     tokens, merged across partitions by log-sum-exp.  Same arguments and
-    result as ``paged_attention_v1`` plus ``partition_size``."""
+    result as ``paged_attention_v1`` plus ``partition_size``.  A workgroup
+    takes a run of consecutive partitions (as many as keep one workgroup per
+    CU) and merges them as it streams; the merge kernel combines the runs by
+    the same rule, so the result is the same softmax either way."""
     partition_size = int(partition_size)
     if partition_size <= 0 or partition_size % 16 or partition_size % int(block_size) or partition_size > 4096:
         raise ValueError("partition_size must be a positive multiple of 16 and of block_size, at most 4096")

@@ -94,15 +94,16 @@ def test_paged_attention_rejections(kw, code, msg):
 
 
 def test_noalloc_refuses_oversize_before_any_hip_call():
-    # 8 sequences x 32 heads at 64K tokens in 16-token partitions need 545 MB
-    # of partials, more than the 32 MiB static scratch: refused by the
+    # 256 sequences x 32 heads at 64K tokens in 4096-token partitions need
+    # 68 MB of partials, more than the 32 MiB static scratch: refused by the
     # argument checks, so this runs without a GPU.
     import numpy as np
     buf = np.zeros(64, dtype=np.uint8)
     p = ctypes.c_void_p((buf.ctypes.data + 15) // 16 * 16)
-    kw = dict(out=p, q=p, kc=p, vc=p, bt=p, ctx=p, B=8, Hq=32, Hkv=8, max_blocks=4096, max_seq_len=65536,
-              q_stride=32 * 128, kbs=8 * 128 * 16, vbs=8 * 128 * 16, ps=16)
-    assert _lib.lib().pkv_paged_attention_workspace_size(8, 32, 8, 128, 65536, 16) > _lib.PKV_NOALLOC_SCRATCH_BYTES
+    kw = dict(out=p, q=p, kc=p, vc=p, bt=p, ctx=p, B=256, Hq=32, Hkv=8, max_blocks=4096, max_seq_len=65536,
+              q_stride=32 * 128, kbs=8 * 128 * 16, vbs=8 * 128 * 16, ps=4096)
+    assert _lib.lib().pkv_paged_attention_workspace_size(256, 32, 8, 128, 65536, 4096) > \
+        _lib.PKV_NOALLOC_SCRATCH_BYTES
     st, err = attn(noalloc=True, **kw)
     assert st == _lib.PKV_ERR_UNSUPPORTED and "static scratch" in err, (st, err)
     assert attn(noalloc=True, B=0)[0] == _lib.PKV_OK
@@ -168,11 +169,18 @@ def test_workspace_size_closed_form():
     # A short context never goes below 256-token partitions.
     assert lib.pkv_paged_attention_workspace_size(1, 8, 1, 64, 1000, 0) == \
         align(8 * 4 * 2 * 4) + align(8 * 4 * 64 * 4)
-    # Explicit split-K partitions.
+    # Explicit split-K partitions: runs of them per workgroup, as many as
+    # keep v1's grid (here 4096 tokens, so 8 of 512 and 1 of 4096) ...
     assert lib.pkv_paged_attention_workspace_size(4, 28, 4, 128, 131072, 512) == \
-        align(4 * 28 * 256 * 2 * 4) + align(4 * 28 * 256 * 128 * 4)
+        align(4 * 28 * 32 * 2 * 4) + align(4 * 28 * 32 * 128 * 4)
     assert lib.pkv_paged_attention_workspace_size(4, 28, 4, 128, 131072, 4096) == \
         align(4 * 28 * 32 * 2 * 4) + align(4 * 28 * 32 * 128 * 4)
+    # ... and whole partitions: 10 of 400 tokens (4000) where v1 takes 4096.
+    assert lib.pkv_paged_attention_workspace_size(4, 28, 4, 128, 65536, 400) == \
+        align(4 * 28 * 17 * 2 * 4) + align(4 * 28 * 17 * 128 * 4)
+    # One sequence at 32K: v1 takes 512, so 512-token partitions are not grouped.
+    assert lib.pkv_paged_attention_workspace_size(1, 28, 4, 128, 32768, 512) == \
+        align(28 * 64 * 2 * 4) + align(28 * 64 * 128 * 4)
     assert lib.pkv_paged_attention_workspace_size(4, 28, 4, 128, 100, 24) == 0
     assert lib.pkv_paged_attention_workspace_size(4, 28, 3, 128, 100, 0) == 0
     assert lib.pkv_paged_attention_workspace_size(4, 28, 4, 128, 100, 8192) == 0

@@ -76,11 +76,11 @@ def test_noalloc_matches_workspace_entry_point(first, ps1, second, ps2):
 
 
 def test_noalloc_refuses_more_than_its_scratch():
-    # 8 sequences x 32 heads at 64K tokens in 16-token partitions would need
-    # 8 * 32 * 4096 * (128 + 2) * 4 bytes (545 MB) of partials.
+    # 256 sequences x 32 heads at 64K tokens in 4096-token partitions would
+    # need 256 * 32 * 16 * (128 + 2) * 4 bytes (68 MB) of partials.
     lib = _lib.lib()
-    B, Hq, Hkv, D, bs, msl = 8, 32, 8, 128, 16, 65536
-    need = lib.pkv_paged_attention_workspace_size(B, Hq, Hkv, D, msl, 16)
+    B, Hq, Hkv, D, bs, msl = 256, 32, 8, 128, 16, 65536
+    need = lib.pkv_paged_attention_workspace_size(B, Hq, Hkv, D, msl, 4096)
     assert need > _lib.PKV_NOALLOC_SCRATCH_BYTES
     q = torch.zeros((B, Hq, D), dtype=torch.bfloat16, device="cuda")
     out = torch.full_like(q, 7.0)
@@ -91,7 +91,7 @@ def test_noalloc_refuses_more_than_its_scratch():
     st = lib.pkv_paged_attention_noalloc(
         out.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(), bt.data_ptr(), lens.data_ptr(), None,
         B, Hq, Hkv, D, bs, bt.shape[1], msl, 2, 1.0, q.stride(0), kc.stride(0), kc.stride(1), vc.stride(0),
-        vc.stride(1), _lib.PKV_LAYOUT_PAGED5D, 16, _lib.PKV_BF16, _lib.PKV_BF16, 1.0, 1.0,
+        vc.stride(1), _lib.PKV_LAYOUT_PAGED5D, 4096, _lib.PKV_BF16, _lib.PKV_BF16, 1.0, 1.0,
         torch.cuda.current_stream().cuda_stream)
     assert st == _lib.PKV_ERR_UNSUPPORTED
     assert "static scratch" in lib.pkv_last_error().decode()
