@@ -1829,6 +1829,9 @@ template <int S> struct GroupItem {
 #ifndef PKV_GROUP_CPOL
 #define PKV_GROUP_CPOL 0
 #endif
+#ifndef PKV_GROUP_ONE_CONSUME
+#define PKV_GROUP_ONE_CONSUME 1
+#endif
 
 
 template <class QT, class CT, int D, int BS, int S, int NW, int NB>
@@ -2112,11 +2115,22 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_group_kernel(DecodeParam
       // such jobs check V for non-finite values (consume_tile); a shared
       // job of an item whose sequences are all live has every column on.
       const bool partial = j.i >= 0 || !all_live;
-      if (j.ntok < kTile)
+      // 16-bit caches: one code path for whole and partial tiles (the token
+      // mask is built for every job).  With a second path the compiler moved
+      // the accumulators between register sets at every join (64 more VGPRs
+      // and 16 v_mov_b64 per job); one path measured 91.0 against 99.0 us on
+      // the radix-shared B256 workload, same process.  FP8 tiles keep the
+      // two paths: their masking comes after the dequantisation and costs
+      // more than the moves (75.8 against 72.0 us).
+      if (PKV_GROUP_ONE_CONSUME && !F8) {
+        consume_tile<QT, CT, D, BS, false, true, true>(p, t, tt0, t1, lane_ctx, g, col, qa, qb, slope, acc, on,
+                                                       partial);
+      } else if (j.ntok < kTile) {
         consume_tile<QT, CT, D, BS, false, true, true>(p, t, tt0, t1, lane_ctx, g, col, qa, qb, slope, acc, on, partial);
-      else
+      } else {
         consume_tile<QT, CT, D, BS, false, false, true>(p, t, tt0, t1, lane_ctx, g, col, qa, qb, slope, acc, on,
                                                         partial);
+      }
     };
 
     // Ring of NB tile buffers: the loads of the next NB - 1 jobs are in
