@@ -516,25 +516,32 @@ def bench_radix(dev, kernels, steps: int = 40, warmup: int = 5, layers: int = 4,
 
 def bench_cpu(res, budget_s):
     """CPU baseline leg: the oracle package's torch-CPU gather + SDPA, same
-    inputs (layer 0), full batch."""
+    inputs (layer 0), full batch.  The reported value follows
+    tests/bench_paged_vs_gather.py:84-103 of the reference: each step relays
+    the paged 5-D caches out as token-major copies, then gathers and runs
+    SDPA per sequence.  token_major_pool times the same decode from pools
+    already token-major (MHATokenPool's layout, memory_pool.py:102-108),
+    built outside the timed region."""
     from oracle import cpu_baseline as cb
 
     inp = res["inp"]
     kc, vc = inp["pools"][0]
-    nb, Hkv, D, bs = inp["nb"], inp["Hkv"], inp["D"], inp["bs"]
-    # Token-major pool [nb*bs, Hkv, D], as MHATokenPool stores it (slot = block*bs + offset).
-    k_pool = kc.permute(0, 3, 1, 2, 4).reshape(nb * bs, Hkv, D).cpu()
-    v_pool = vc.permute(0, 3, 1, 2).reshape(nb * bs, Hkv, D).cpu()
+    bs = inp["bs"]
+    k5, v5 = kc.cpu(), vc.cpu()
     q, bt, ctx = inp["q"].cpu(), inp["bt"].cpu(), inp["ctx"].cpu()
-    t = cb.time_decode(q, k_pool, v_pool, bt, ctx, bs, res["scale"], budget_s=budget_s)
-    cpu_out = cb.gather_sdpa_decode(q, k_pool, v_pool, bt, ctx, bs, res["scale"])
+    t = cb.time_decode(q, k5, v5, bt, ctx, bs, res["scale"], budget_s=budget_s, fn=cb.gather_sdpa_decode_paged5d)
+    cpu_out = cb.gather_sdpa_decode_paged5d(q, k5, v5, bt, ctx, bs, res["scale"])
+    k_pool, v_pool = cb.paged5d_to_token_major(k5, v5)
+    tm = cb.time_decode(q, k_pool, v_pool, bt, ctx, bs, res["scale"], budget_s=budget_s / 2)
     diff = (cpu_out.float() - res["out0"].float().cpu()).abs().max().item()
     gbs = res["nbytes"] / t["median_s"] / 1e9
     return dict(value=round(gbs, 2), unit="GB/s", cores=t["threads"], kind="port",
-                sample=(f"full batch (64 seqs, one layer), gather+SDPA per sequence in torch-CPU bf16, "
-                        f"median of {t['iters']} iterations"),
+                sample=(f"full batch (64 seqs, one layer): relayout of the paged 5-D caches to token-major, "
+                        f"then gather+SDPA per sequence, torch-CPU bf16, median of {t['iters']} iterations"),
                 us_per_step=round(t["median_s"] * 1e6, 1), cpu=t["cpu"],
                 label="CPU restatement of the reference's gather+SDPA path (MLX CPU backend unavailable offline)",
+                token_major_pool=dict(us_per_step=round(tm["median_s"] * 1e6, 1),
+                                      gbs=round(res["nbytes"] / tm["median_s"] / 1e9, 2), iters=tm["iters"]),
                 max_abs_diff_vs_gpu=round(diff, 5))
 
 

@@ -1,8 +1,8 @@
 """CPU baseline: torch-CPU restatement of the reference's gather + SDPA decode.
 
 TEST INFRASTRUCTURE ONLY -- used by the ``cpu_baseline`` leg of bench.py
-(and by the CPU tests that check it against the float64 oracle).  Nothing in
-the product package imports it.
+and by tests/test_cpu_baseline.py, which checks it against the float64
+oracle.  Nothing in the product package imports it.
 
 The reference decodes without its paged kernel: each layer scatters the new
 token into the token-major MHATokenPool buffers, gathers every token of the
@@ -20,6 +20,12 @@ backend), so this restatement runs the same steps with torch on the host:
      transpose to [1, Hkv, T, D];
   3. torch.nn.functional.scaled_dot_product_attention(q[1, Hq, 1, D], k, v,
      scale, enable_gqa=True).
+
+tests/bench_paged_vs_gather.py:86-92 starts one step earlier: its gather
+first relays the paged 5-D caches out as token-major [nb * bs, Hkv, D]
+(a transpose + copy of the whole cache) and then indexes them.
+gather_sdpa_decode_paged5d does the same, so that the relayout is inside
+whatever is timed.
 
 The 1e-6 in the reference kernel's softmax denominator is a kernel detail
 (paged_attention_kernels.metal:144), absent from SDPA, so results differ
@@ -87,20 +93,41 @@ def gather_sdpa_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tens
     return out
 
 
+def paged5d_to_token_major(key_cache: torch.Tensor, value_cache: torch.Tensor):
+    """The paged 5-D caches K [nb, Hkv, D/x, bs, x] and V [nb, Hkv, D, bs]
+    as token-major [nb * bs, Hkv, D] copies (slot = block * bs + offset),
+    the relayout of tests/bench_paged_vs_gather.py:86-92."""
+    nb, hkv, dx, bs, x = key_cache.shape
+    k = key_cache.permute(0, 3, 1, 2, 4).reshape(nb * bs, hkv, dx * x)
+    v = value_cache.permute(0, 3, 1, 2).reshape(nb * bs, hkv, dx * x)
+    return k, v
+
+
+def gather_sdpa_decode_paged5d(q, key_cache, value_cache, block_tables, context_lens, block_size, scale,
+                               seqs=None):
+    """gather_sdpa_decode from the paged 5-D caches: relayout to token-major
+    first, as the reference's benchmark does, then gather + SDPA."""
+    k_pool, v_pool = paged5d_to_token_major(key_cache, value_cache)
+    return gather_sdpa_decode(q, k_pool, v_pool, block_tables, context_lens, block_size, scale, seqs)
+
+
 def time_decode(q, k_pool, v_pool, block_tables, context_lens, block_size, scale,
-                budget_s: float = 10.0, min_iters: int = 5, seqs=None) -> dict:
-    """Median wall time of gather_sdpa_decode over >= min_iters runs (after
-    one warm-up), stopping once ``budget_s`` of timed work is done."""
+                budget_s: float = 10.0, min_iters: int = 5, seqs=None, fn=None) -> dict:
+    """Median wall time of ``fn`` (gather_sdpa_decode by default; its
+    k_pool / v_pool are then token-major pools, for
+    gather_sdpa_decode_paged5d the paged 5-D caches) over >= min_iters runs
+    (after one warm-up), stopping once ``budget_s`` of timed work is done."""
+    fn = fn or gather_sdpa_decode
     threads = host_threads()
     prev = torch.get_num_threads()
     torch.set_num_threads(threads)
     try:
-        gather_sdpa_decode(q, k_pool, v_pool, block_tables, context_lens, block_size, scale, seqs)
+        fn(q, k_pool, v_pool, block_tables, context_lens, block_size, scale, seqs)
         times = []
         t_all = time.perf_counter()
         while len(times) < min_iters or time.perf_counter() - t_all < budget_s:
             t0 = time.perf_counter()
-            gather_sdpa_decode(q, k_pool, v_pool, block_tables, context_lens, block_size, scale, seqs)
+            fn(q, k_pool, v_pool, block_tables, context_lens, block_size, scale, seqs)
             times.append(time.perf_counter() - t0)
             if len(times) >= 1000:
                 break
