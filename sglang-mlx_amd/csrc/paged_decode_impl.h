@@ -1722,7 +1722,10 @@ __global__ __launch_bounds__(64 * (Persist<D, BS == 0>::kWaves)) void paged_deco
   const int total = B * p.units;
   const int G = gridDim.x;
 
-  const bool ordered = rank_sequences(p, s_ctx, s_order, tid, NT);
+  // With at most one item per workgroup the order balances nothing, so the
+  // ranking (a context-length load and two barriers) is skipped and items
+  // go in index order.
+  const bool ordered = total > G && rank_sequences(p, s_ctx, s_order, tid, NT);
   // Rank of this workgroup's k-th item (>= total: none).
   auto rank_of = [&](int k) { return k * G + ((k & 1) ? G - 1 - (int)blockIdx.x : (int)blockIdx.x); };
   auto item_at = [&](int rank) {
