@@ -586,11 +586,27 @@ template <int D, bool ROWS> __device__ __forceinline__ constexpr int tile_dim(in
   return 16 * dt + 4 * g;
 }
 
+// Token rows at head sizes that are multiples of 32 load V whole-row
+// (load_tile_rows_whole): lane (g, n) takes dimensions n*NDL .. n*NDL+NDL-1
+// (NDL = D / 16) of tokens 4g .. 4g+3, so a quarter-wavefront reads one
+// token's row in one piece, and v_perm alone regroups the four tokens into
+// operand tiles: tile dt, row n stands for dimension n*NDL + dt.  Output
+// row 4g + r of tile dt is then dimension (4g + r)*NDL + dt, no longer four
+// consecutive dimensions, so the writers store element by element.
+template <int D, bool ROWS> struct RowsWhole {
+  static constexpr bool value = ROWS && D % 32 == 0;
+};
+template <int D, bool ROWS> __device__ __forceinline__ constexpr int out_dim(int dt, int g, int r) {
+  if constexpr (RowsWhole<D, ROWS>::value) return (4 * g + r) * (D / 16) + dt;
+  return tile_dim<D, ROWS>(dt, g) + r;
+}
+
 // rk: row of token col (the lane's K token); rv: row of token 4g + (col & 3)
 // (the lane's V token).  V: lane (g, 4a + i) loads dimensions 32e + 8a .. +7
 // of token 4g + i into tiles 2e (first four) and 2e + 1 (last four), see
-// tile_dim; an odd last tile takes dimensions 16dt + 4a .. +3.
-template <int D>
+// tile_dim; an odd last tile takes dimensions 16dt + 4a .. +3.  V = false:
+// K only (whole-row V comes from load_v_whole).
+template <int D, bool V = true>
 __device__ __forceinline__ void load_tile_rows(Tile<D>& t, const uint16_t* kbase, const uint16_t* vbase,
                                                int64_t k_row_stride, int64_t v_row_stride, int rk, int rv,
                                                int g, int col) {
@@ -604,6 +620,7 @@ __device__ __forceinline__ void load_tile_rows(Tile<D>& t, const uint16_t* kbase
     const int c = 4 * j + g;
     t.k[j] = (NCHUNK % 4 == 0 || c < NCHUNK) ? *reinterpret_cast<const uint4*>(kp + c * 8) : make_uint4(0, 0, 0, 0);
   }
+  if constexpr (!V) return;
   constexpr int PAIRS = Tile<D>::DT / 2;
 #pragma unroll
   for (int e = 0; e < PAIRS; ++e) {
@@ -621,8 +638,8 @@ __device__ __forceinline__ void load_tile_rows(Tile<D>& t, const uint16_t* kbase
 
 // load_tile_rows through buffer resources with 32-bit byte offsets (the
 // persistent kernel's form; k_bytes/v_bytes bound the reachable range):
-// one VGPR per address and no 64-bit arithmetic per tile.
-template <int D, int CPOL = 0>
+// one VGPR per address and no 64-bit arithmetic per tile.  V = false: K only.
+template <int D, int CPOL = 0, bool V = true>
 __device__ __forceinline__ void load_tile_rows_buf(Tile<D>& t, __amdgpu_buffer_rsrc_t kr, __amdgpu_buffer_rsrc_t vr,
                                                    uint32_t k_row_bytes, uint32_t v_row_bytes, int rk, int rv, int g,
                                                    int col) {
@@ -644,6 +661,7 @@ __device__ __forceinline__ void load_tile_rows_buf(Tile<D>& t, __amdgpu_buffer_r
                  ? __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(kr, ko + j * 64, 0, CPOL))
                  : make_uint4(0, 0, 0, 0);
   }
+  if constexpr (!V) return;
   constexpr int PAIRS = Tile<D>::DT / 2;
 #pragma unroll
   for (int e = 0; e < PAIRS; ++e) {
@@ -665,10 +683,93 @@ __device__ __forceinline__ void load_tile_rows_buf(Tile<D>& t, __amdgpu_buffer_r
 }
 
 // Turns the V rows load_tile_rows left in t.v into the PV operand.
-template <int D> __device__ __forceinline__ void transpose_tile_rows(Tile<D>& t, int col) {
-  const uint32_t sel = quad_transpose_sel(col & 3);
+// Whole-row V (RowsWhole): the raw words of token 4g + e, dimensions
+// (2m, 2m + 1) of the lane's n*NDL .. run, go to word e*W + m of t.v
+// (W = NDL / 2 words per token); transpose_tile_rows regroups them.
+template <int D> __device__ __forceinline__ void set_raw(Tile<D>& t, int i, uint32_t w) {
+  if (i & 1)
+    t.v[i >> 1].y = w;
+  else
+    t.v[i >> 1].x = w;
+}
+template <int D> __device__ __forceinline__ uint32_t raw_at(const Tile<D>& t, int i) {
+  return (i & 1) ? t.v[i >> 1].y : t.v[i >> 1].x;
+}
+// Through a buffer resource with 32-bit offsets (rv: rows of tokens 4g ..
+// 4g+3, -1 masked; masked rows read row 0, which the K-row masks discard).
+template <int D, int CPOL = 0>
+__device__ __forceinline__ void load_v_whole_buf(Tile<D>& t, __amdgpu_buffer_rsrc_t vr, uint32_t v_row_bytes, int4 rv,
+                                                 int col) {
+  constexpr int NDL = D / 16, W = NDL / 2;
+  const int rows[4] = {rv.x, rv.y, rv.z, rv.w};
 #pragma unroll
-  for (int dt = 0; dt < Tile<D>::DT; ++dt) t.v[dt] = quad_transpose16(t.v[dt], col & 3, sel);
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t vo = (uint32_t)(rows[e] < 0 ? 0 : rows[e]) * v_row_bytes + (uint32_t)col * (NDL * 2);
+    uint32_t w[W];
+    if constexpr (W == 1) {
+      w[0] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(vr, vo, 0, CPOL);
+    } else if constexpr (W == 2) {
+      const uint2 x = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(vr, vo, 0, CPOL));
+      w[0] = x.x, w[1] = x.y;
+    } else if constexpr (W == 3) {
+      const auto x = __builtin_amdgcn_raw_buffer_load_b96(vr, vo, 0, CPOL);
+      w[0] = x[0], w[1] = x[1], w[2] = x[2];
+    } else {
+      static_assert(W % 2 == 0, "W = 4, 6 or 8 words per token");
+#pragma unroll
+      for (int h = 0; h < W / 4; ++h) {
+        const uint4 x = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(vr, vo + h * 16, 0, CPOL));
+        w[4 * h] = x.x, w[4 * h + 1] = x.y, w[4 * h + 2] = x.z, w[4 * h + 3] = x.w;
+      }
+      if constexpr (W % 4 == 2) {
+        const uint2 x =
+            __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(vr, vo + (W / 4) * 16, 0, CPOL));
+        w[W - 2] = x.x, w[W - 1] = x.y;
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < W; ++m) set_raw<D>(t, e * W + m, w[m]);
+  }
+}
+// Through 64-bit addresses (vbase: the head's base; v_row_stride in
+// elements, a multiple of 8).
+template <int D>
+__device__ __forceinline__ void load_v_whole(Tile<D>& t, const uint16_t* vbase, int64_t v_row_stride, int4 rv,
+                                             int col) {
+  constexpr int NDL = D / 16, W = NDL / 2;
+  const int rows[4] = {rv.x, rv.y, rv.z, rv.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t* vp =
+        reinterpret_cast<const uint32_t*>(vbase + (int64_t)(rows[e] < 0 ? 0 : rows[e]) * v_row_stride + col * NDL);
+#pragma unroll
+    for (int m = 0; m < W; ++m) set_raw<D>(t, e * W + m, vp[m]);
+  }
+}
+
+template <int D> __device__ __forceinline__ void transpose_tile_rows(Tile<D>& t, int col) {
+  if constexpr (D % 32 == 0) {
+    // Whole-row V: word m of the four tokens holds dimensions (2m, 2m+1);
+    // tile 2m takes their low halves (tokens 4g, 4g+1 | 4g+2, 4g+3), tile
+    // 2m + 1 the high ones.
+    constexpr int W = D / 32;
+    uint32_t r[4][W];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int m = 0; m < W; ++m) r[e][m] = raw_at<D>(t, e * W + m);
+#pragma unroll
+    for (int m = 0; m < W; ++m) {
+      t.v[2 * m] = make_uint2(__builtin_amdgcn_perm(r[1][m], r[0][m], 0x05040100u),
+                              __builtin_amdgcn_perm(r[3][m], r[2][m], 0x05040100u));
+      t.v[2 * m + 1] = make_uint2(__builtin_amdgcn_perm(r[1][m], r[0][m], 0x07060302u),
+                                  __builtin_amdgcn_perm(r[3][m], r[2][m], 0x07060302u));
+    }
+  } else {
+    const uint32_t sel = quad_transpose_sel(col & 3);
+#pragma unroll
+    for (int dt = 0; dt < Tile<D>::DT; ++dt) t.v[dt] = quad_transpose16(t.v[dt], col & 3, sel);
+  }
 }
 
 // Row ids of a tile's tokens for the token-row layout, staged in LDS by the
@@ -680,7 +781,12 @@ struct LdsRows {
   __device__ __forceinline__ void load_tile(Tile<D>& t, const DecodeParams& p, const uint16_t* kbase,
                                             const uint16_t* vbase, int tile, int /*k*/, int g, int col) const {
     const int32_t* r = rows + tile * kTile;
-    load_tile_rows<D>(t, kbase, vbase, p.k_block_stride, p.v_block_stride, r[col], r[4 * g + (col & 3)], g, col);
+    if constexpr (D % 32 == 0) {
+      load_tile_rows<D, false>(t, kbase, vbase, p.k_block_stride, p.v_block_stride, r[col], 0, g, col);
+      load_v_whole<D>(t, vbase, p.v_block_stride, *reinterpret_cast<const int4*>(r + 4 * g), col);
+    } else {
+      load_tile_rows<D>(t, kbase, vbase, p.k_block_stride, p.v_block_stride, r[col], r[4 * g + (col & 3)], g, col);
+    }
   }
 };
 
@@ -721,17 +827,38 @@ template <int MAXT> struct WaveRows {
   template <int D, int CPOL = 0>
   __device__ __forceinline__ void load_tile(Tile<D>& t, const DecodeParams& p, const uint16_t* /*kbase*/,
                                             const uint16_t* /*vbase*/, int /*tile*/, int k, int g, int col) const {
-    const int2 r = at(k, g, col);
-    load_tile_rows_buf<D, CPOL>(t, kr, vr, (uint32_t)p.k_block_stride * 2u, (uint32_t)p.v_block_stride * 2u, r.x, r.y, g,
-                          col);
+    if constexpr (D % 32 == 0) {
+      const int x = pick(k);
+      const int base = (k & 3) * kTile;
+      load_tile_rows_buf<D, CPOL, false>(t, kr, vr, (uint32_t)p.k_block_stride * 2u, 0u, __shfl(x, base + col), 0, g,
+                                         col);
+      const int4 rv = make_int4(__shfl(x, base + 4 * g), __shfl(x, base + 4 * g + 1), __shfl(x, base + 4 * g + 2),
+                                __shfl(x, base + 4 * g + 3));
+      load_v_whole_buf<D, CPOL>(t, vr, (uint32_t)p.v_block_stride * 2u, rv, col);
+    } else {
+      const int2 r = at(k, g, col);
+      load_tile_rows_buf<D, CPOL>(t, kr, vr, (uint32_t)p.k_block_stride * 2u, (uint32_t)p.v_block_stride * 2u, r.x,
+                                  r.y, g, col);
+    }
   }
-  // (K row, V row) of the lane for the wavefront's k-th tile (wave-uniform k).
-  __device__ __forceinline__ int2 at(int k, int g, int col) const {
+  // The register holding the wavefront's k-th tile (wave-uniform k).
+  __device__ __forceinline__ int pick(int k) const {
     const int c = k >> 2;
     int x = v[0];
 #pragma unroll
-    for (int i = 1; i < N; ++i)
-      if (c == i) x = v[i];
+    for (int i = 1; i < N; ++i) {
+      // An opaque copy keeps this a select of registers: a select of the
+      // array's elements is otherwise folded into an indexed load, which
+      // moves the array to scratch memory.
+      int y = v[i];
+      asm("" : "+v"(y));
+      if (c == i) x = y;
+    }
+    return x;
+  }
+  // (K row, V row) of the lane for the wavefront's k-th tile.
+  __device__ __forceinline__ int2 at(int k, int g, int col) const {
+    const int x = pick(k);
     const int base = (k & 3) * kTile;
     return make_int2(__shfl(x, base + col), __shfl(x, base + 4 * g + (col & 3)));
   }
@@ -1325,7 +1452,7 @@ __device__ __forceinline__ void write_output(const DecodeParams& p, int64_t hrow
   for (int dt = 0; dt < Tile<D>::DT; ++dt)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int d = tile_dim<D, ROWS>(dt, g) + r;
+      const int d = out_dim<D, ROWS>(dt, g, r);
       if (D % 16 == 0 || d < D) out[d] = from_f32<QT>(acc.o[dt][r] * inv);
     }
 }
@@ -1406,7 +1533,14 @@ __device__ __forceinline__ void merge_store_waves(const DecodeParams& p, WaveAcc
       o.z += aw[w] * x.z;
       o.w += aw[w] * x.w;
     }
-    store4<QT>(out + d0, o.x * inv, o.y * inv, o.z * inv, o.w * inv);
+    if constexpr (RowsWhole<D, ROWS>::value) {
+      out[out_dim<D, ROWS>(dt, g, 0)] = from_f32<QT>(o.x * inv);
+      out[out_dim<D, ROWS>(dt, g, 1)] = from_f32<QT>(o.y * inv);
+      out[out_dim<D, ROWS>(dt, g, 2)] = from_f32<QT>(o.z * inv);
+      out[out_dim<D, ROWS>(dt, g, 3)] = from_f32<QT>(o.w * inv);
+    } else {
+      store4<QT>(out + d0, o.x * inv, o.y * inv, o.z * inv, o.w * inv);
+    }
   }
 }
 
@@ -1516,7 +1650,7 @@ __global__ __launch_bounds__(64 * kPartWaves) void paged_decode_rows_kernel(Deco
   __shared__ float s_red[NW - 1][DT * 4][64];
   __shared__ float s_m[NW][16];
   __shared__ float s_l[NW][16];
-  __shared__ int32_t s_rows[kMaxPartition];
+  __shared__ __align__(16) int32_t s_rows[kMaxPartition];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1583,10 +1717,15 @@ __global__ __launch_bounds__(64 * kPartWaves) void paged_decode_rows_kernel(Deco
   float* wo = p.ws_o + slot * D;
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) {
-    const int d = tile_dim<D, true>(dt, g);
-    if (D % 16 == 0 || d < D)
-      *reinterpret_cast<float4*>(wo + d) =
-          make_float4(acc.o[dt][0] * invl, acc.o[dt][1] * invl, acc.o[dt][2] * invl, acc.o[dt][3] * invl);
+    if constexpr (RowsWhole<D, true>::value) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) wo[out_dim<D, true>(dt, g, r)] = acc.o[dt][r] * invl;
+    } else {
+      const int d = tile_dim<D, true>(dt, g);
+      if (D % 16 == 0 || d < D)
+        *reinterpret_cast<float4*>(wo + d) =
+            make_float4(acc.o[dt][0] * invl, acc.o[dt][1] * invl, acc.o[dt][2] * invl, acc.o[dt][3] * invl);
+    }
   }
   if (g == 0) *reinterpret_cast<float2*>(p.ws_ml + slot * 2) = make_float2(M, L);
 }
