@@ -790,15 +790,17 @@ struct LdsRows {
   }
 };
 
-// Row ids of the tiles one wavefront streams, held in registers: entry
-// e = 64 * c + lane of array c is token e % 16 of the wavefront's tile number
-// e / 16 (0-based in the order the wavefront takes them), so one VGPR holds
-// four tiles and a tile's ids reach the lanes that need them through two
-// lane permutes.  Ids outside the cache (block ids outside [0, num_blocks))
-// are -1.
+// Row ids of the tiles one wavefront streams, in the wavefront's own LDS
+// region (`ids`, N * 64 entries, 16-byte aligned): entry e is token e % 16 of
+// the wavefront's tile number e / 16 (0-based in the order the wavefront
+// takes them), so a tile's ids are 16 consecutive entries, and each lane
+// reads its K row (one entry) and its four V rows (one 16-byte read)
+// directly.  Ids outside the cache (block ids outside [0, num_blocks)) are
+// -1.  (Held in registers instead, a tile's ids took a select over the
+// registers and five lane permutes: ~40 more instructions per tile.)
 template <int MAXT> struct WaveRows {
   static constexpr int N = (MAXT * kTile + 63) / 64;
-  int v[N];
+  int32_t* ids;
   // 32-bit buffer views of the item's K and V head (set with the item).
   __amdgpu_buffer_rsrc_t kr, vr;
 
@@ -806,7 +808,8 @@ template <int MAXT> struct WaveRows {
   // row `row` (block size 1 << shift): token t lives in row
   // bt[t >> shift] << shift | t & (block size - 1).  The loads are
   // unconditional (tokens past the bound read its last entry) so that they
-  // issue back to back.
+  // issue back to back.  Only this wavefront reads the entries it writes,
+  // so no barrier is needed.
   __device__ __forceinline__ void load(const int32_t* row, int shift, int64_t num_blocks, int bound, int first,
                                        int nw, int lane) {
     int b[N];
@@ -821,46 +824,21 @@ template <int MAXT> struct WaveRows {
       const int e = 64 * c + lane;
       const int t = (first + (e >> 4) * nw) * kTile + (e & 15);
       const bool ok = t < bound && (int64_t)(uint32_t)b[c] < num_blocks;
-      v[c] = ok ? (b[c] << shift) + (t & ((1 << shift) - 1)) : -1;
+      ids[e] = ok ? (b[c] << shift) + (t & ((1 << shift) - 1)) : -1;
     }
   }
   template <int D, int CPOL = 0>
   __device__ __forceinline__ void load_tile(Tile<D>& t, const DecodeParams& p, const uint16_t* /*kbase*/,
                                             const uint16_t* /*vbase*/, int /*tile*/, int k, int g, int col) const {
+    const int32_t* r = ids + k * kTile;
     if constexpr (D % 32 == 0) {
-      const int x = pick(k);
-      const int base = (k & 3) * kTile;
-      load_tile_rows_buf<D, CPOL, false>(t, kr, vr, (uint32_t)p.k_block_stride * 2u, 0u, __shfl(x, base + col), 0, g,
-                                         col);
-      const int4 rv = make_int4(__shfl(x, base + 4 * g), __shfl(x, base + 4 * g + 1), __shfl(x, base + 4 * g + 2),
-                                __shfl(x, base + 4 * g + 3));
+      const int4 rv = *reinterpret_cast<const int4*>(r + 4 * g);
+      load_tile_rows_buf<D, CPOL, false>(t, kr, vr, (uint32_t)p.k_block_stride * 2u, 0u, r[col], 0, g, col);
       load_v_whole_buf<D, CPOL>(t, vr, (uint32_t)p.v_block_stride * 2u, rv, col);
     } else {
-      const int2 r = at(k, g, col);
-      load_tile_rows_buf<D, CPOL>(t, kr, vr, (uint32_t)p.k_block_stride * 2u, (uint32_t)p.v_block_stride * 2u, r.x,
-                                  r.y, g, col);
+      load_tile_rows_buf<D, CPOL>(t, kr, vr, (uint32_t)p.k_block_stride * 2u, (uint32_t)p.v_block_stride * 2u, r[col],
+                                  r[4 * g + (col & 3)], g, col);
     }
-  }
-  // The register holding the wavefront's k-th tile (wave-uniform k).
-  __device__ __forceinline__ int pick(int k) const {
-    const int c = k >> 2;
-    int x = v[0];
-#pragma unroll
-    for (int i = 1; i < N; ++i) {
-      // An opaque copy keeps this a select of registers: a select of the
-      // array's elements is otherwise folded into an indexed load, which
-      // moves the array to scratch memory.
-      int y = v[i];
-      asm("" : "+v"(y));
-      if (c == i) x = y;
-    }
-    return x;
-  }
-  // (K row, V row) of the lane for the wavefront's k-th tile.
-  __device__ __forceinline__ int2 at(int k, int g, int col) const {
-    const int x = pick(k);
-    const int base = (k & 3) * kTile;
-    return make_int2(__shfl(x, base + col), __shfl(x, base + 4 * g + (col & 3)));
   }
 };
 
@@ -1834,7 +1812,7 @@ struct PersistItem {
 };
 
 // BS = 0: token-row caches (any block size, p.block_size), with each
-// wavefront's row ids in registers (WaveRows); otherwise the paged layout.
+// wavefront's row ids in LDS (WaveRows); otherwise the paged layout.
 template <class QT, class CT, int D, int BS>
 __global__ __launch_bounds__(64 * (Persist<D, BS == 0>::kWaves)) void paged_decode_persist_kernel(DecodeParams p) {
   constexpr int NW = Persist<D, BS == 0>::kWaves;
@@ -1852,6 +1830,9 @@ __global__ __launch_bounds__(64 * (Persist<D, BS == 0>::kWaves)) void paged_deco
   __shared__ float s_l[2][NW][16];
   __shared__ __align__(16) uint32_t s_ctx[kPersistMaxOrder];
   __shared__ int32_t s_order[kPersistMaxOrder];
+  // Token rows: each wavefront's row ids (WaveRows).
+  constexpr int kRowIds = ROWS ? 64 * ((MAXT * kTile + 63) / 64) : 4;
+  __shared__ __align__(16) int32_t s_rowids[NW][kRowIds];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1901,6 +1882,7 @@ __global__ __launch_bounds__(64 * (Persist<D, BS == 0>::kWaves)) void paged_deco
     if (rank >= total) break;
     const PersistItem it = item_at(rank);
     Blocks blk;
+    if constexpr (ROWS) blk.ids = s_rowids[wave];
     load_blocks(it.seq, blk);
     uint4 qa[KSTEPS];
     uint4 qb[SPLIT_Q ? KSTEPS : 1];
