@@ -201,7 +201,7 @@ __global__ __launch_bounds__(64 * PKV_RAC_WAVES) void rac_token_major_wave_kerne
 }
 
 // ---- token-major layout: one wavefront per (token, head) ----------------------------
-// The north star's decomposition, kept for comparison with the one above:
+// The per-(token, head) decomposition, kept for comparison with the one above:
 // lanes 0 .. D/VE-1 move the head's K vectors and the next D/VE lanes its V
 // vectors (32 of 64 lanes at D = 128 with 16-bit caches), same
 // load / barrier / nontemporal-store phases.
