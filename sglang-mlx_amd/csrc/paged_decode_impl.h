@@ -995,8 +995,10 @@ __device__ __forceinline__ void load_query(const DecodeParams& p, int seq, int h
 // (g, col), register r = token vtok + r, head col) -> weights pr against the
 // running reference maximum, updating acc's maxima, sum and (on a raised
 // reference) its accumulators.  kpb / vpb / zero_v: the tile's masking state
-// as consume_tile describes it.
-template <int D, int BS, bool TAIL, bool COLMASK>
+// as consume_tile describes it.  KU: every K row of the tile lies in block
+// vpb (paged tiles of blocks of 16 and more), so vpb alone says whether the
+// rows are live and no lane needs another's kpb.
+template <int D, int BS, bool TAIL, bool COLMASK, bool KU = false>
 __device__ __forceinline__ void softmax_tile(const DecodeParams& p, f32x4 sacc, int vtok, int t1, uint32_t ctx,
                                              int g, float slope, int kpb, int vpb, bool zero_v, bool col_on,
                                              WaveAcc<D>& acc, float (&pr)[4]) {
@@ -1019,7 +1021,7 @@ __device__ __forceinline__ void softmax_tile(const DecodeParams& p, f32x4 sacc, 
     // row of token tt0 + i was loaded by lane col = i.
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int krow_ok = __shfl(kpb, 4 * g + r, 16) >= 0;
+      const bool krow_ok = KU || __shfl(kpb, 4 * g + r, 16) >= 0;
       sc[r] = (vtok + r < t1 && vpb >= 0 && krow_ok) ? sc[r] : -INFINITY;
     }
   } else if constexpr (BS >= kTile) {
@@ -1112,7 +1114,8 @@ __device__ __forceinline__ void consume_tile_h(const DecodeParams& p, Tile<D, st
   }
   // ---- online softmax (log2 domain) ----
   float pr[4];
-  softmax_tile<D, BS, TAIL, COLMASK>(p, sacc, vtok, t1, ctx, g, slope, t.kpb, t.vpb, zero_v, col_on, acc, pr);
+  softmax_tile<D, BS, TAIL, COLMASK, !ROWS && BS >= kTile>(p, sacc, vtok, t1, ctx, g, slope, t.kpb, t.vpb, zero_v,
+                                                          col_on, acc, pr);
   // ---- O^T += V^T * P^T ----
   const uint2 pp = make_uint2(pack_p<MT>(pr[0], pr[1]), pack_p<MT>(pr[2], pr[3]));
   if constexpr (COLMASK) {
@@ -1175,7 +1178,7 @@ __device__ __forceinline__ void consume_tile_f32(const DecodeParams& p, TileF32<
   }
   const f32x4 sacc = (s4[0] + s4[1]) + (s4[2] + s4[3]);
   float pr[4];
-  softmax_tile<D, BS, TAIL, false>(p, sacc, vtok, t1, ctx, g, slope, t.kpb, t.vpb, zero_v, true, acc, pr);
+  softmax_tile<D, BS, TAIL, false, BS >= kTile>(p, sacc, vtok, t1, ctx, g, slope, t.kpb, t.vpb, zero_v, true, acc, pr);
   // ---- O^T += V^T * P^T: MFMA r takes tokens 4g + r ----
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) {
