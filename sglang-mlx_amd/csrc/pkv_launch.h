@@ -21,9 +21,10 @@ constexpr int kMaxParts = 65536;
 // in LDS) and the most sequences it orders longest-first.
 constexpr int kPersistMaxSeq = 16384;
 constexpr int kPersistMaxOrder = 1024;
-// Token-row caches keep each wavefront's row ids in registers (8 VGPRs per
-// item), so their persistent path stops at 4096 tokens with eight wavefronts
-// per workgroup (head sizes up to 128) and at 2048 with four.
+// Token-row caches keep each wavefront's row ids of an item in its own LDS
+// region (512 ids, 2 KiB), so their persistent path stops at 4096 tokens
+// with eight wavefronts per workgroup (head sizes up to 128) and at 2048
+// with four.
 constexpr int persist_rows_max_seq(int head_size) { return head_size > 128 ? 2048 : 4096; }
 
 struct RacParams {
