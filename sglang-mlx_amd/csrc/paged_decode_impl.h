@@ -1964,6 +1964,22 @@ template <int S> struct GroupItem {
 #ifndef PKV_GROUP_PER_CU
 #define PKV_GROUP_PER_CU 1
 #endif
+// FP8 caches: two workgroups of four wavefronts per CU (the same eight
+// wavefronts, two items in flight per CU, so one item's job-list build and
+// merge overlap the other's stream): 66.7 against 70.4 us on the
+// radix-shared B256 workload, same process.  16-bit caches keep one
+// workgroup of eight (with four the kernel spills and times the same), and
+// so do FP8 head sizes that are not multiples of 64 (they would spill).
+template <class CT, int D> struct GroupShape {
+  static constexpr bool kPairs = std::is_same<CT, FP8>::value && D % 64 == 0;
+  static constexpr int kWaves = kPairs ? 4 : PKV_GROUP_WAVES;
+  static constexpr int kPerCu = kPairs ? 2 : PKV_GROUP_PER_CU;
+};
+// Longest context of the grouped kernel with NW wavefronts: each wavefront
+// lists at most 64 tiles of an item (one per lane).
+template <int NW> constexpr int group_max_seq() {
+  return kGroupMaxSeq < 64 * kTile * NW ? kGroupMaxSeq : 64 * kTile * NW;
+}
 // Cache policy of the grouped kernel's tile loads: 0 = nontemporal for
 // private tiles only, 1 = nontemporal for all, 2 = default for all.
 #ifndef PKV_GROUP_CPOL
@@ -1975,14 +1991,14 @@ template <int S> struct GroupItem {
 
 
 template <class QT, class CT, int D, int BS, int S, int NW, int NB>
-__global__ __launch_bounds__(64 * NW) void paged_decode_group_kernel(DecodeParams p) {
+__global__ __launch_bounds__(64 * NW, NW >= 8 ? 1 : 2) void paged_decode_group_kernel(DecodeParams p) {
   static_assert(NB >= 2, "the job pipeline needs at least two tile buffers");
   constexpr int NT = 64 * NW;
   constexpr int KSTEPS = Tile<D>::KSTEPS;
   constexpr int DT = Tile<D>::DT;
   constexpr bool SPLIT_Q = std::is_same<QT, F32>::value;
   constexpr bool F8 = std::is_same<CT, FP8>::value;
-  constexpr int MAXT = kGroupMaxSeq / kTile / NW;  // tiles per wavefront
+  constexpr int MAXT = group_max_seq<NW>() / kTile / NW;  // tiles per wavefront
   using Blocks = WaveBlocks<BS, MAXT>;
   constexpr int PT = Blocks::PER_TILE;
   using TileT = Tile<D, F8>;
@@ -2475,14 +2491,14 @@ inline int device_cus() {
 // Launches the persistent kernel (BS = 0: token rows) when the batch has
 // enough items for it; *launched says whether it did.
 // The grouped kernel when the batch fills it (at least two items of S
-// sequences per resident workgroup), GQA groups fit S to the 16 columns and
-// contexts fit its register-held block ids.
+// sequences per CU), GQA groups fit S to the 16 columns and contexts fit its
+// register-held block ids.
 template <class QT, class CT, int D, int BS>
 static hipError_t launch_grouped(const DecodeParams& p, hipStream_t stream, bool* launched) {
   *launched = false;
   constexpr int S = kGroupSeqs;
-  if (p.slices != 1 || p.group * S > 16 || p.max_seq_len > kGroupMaxSeq) return hipSuccess;
-  constexpr int NW = PKV_GROUP_WAVES, NB = PKV_GROUP_NBUF;
+  constexpr int NW = GroupShape<CT, D>::kWaves, NB = PKV_GROUP_NBUF;
+  if (p.slices != 1 || p.group * S > 16 || p.max_seq_len > group_max_seq<NW>()) return hipSuccess;
   constexpr int NT = 64 * NW;
   static int per_cu = -1;
   if (per_cu < 0) {
@@ -2494,8 +2510,8 @@ static hipError_t launch_grouped(const DecodeParams& p, hipStream_t stream, bool
     per_cu = n;
   }
   const int64_t items = (int64_t)((p.num_seqs + S - 1) / S) * p.num_kv_heads;
-  const int64_t grid = (int64_t)device_cus() * std::min(per_cu, PKV_GROUP_PER_CU);
-  if (grid <= 0 || items < 2 * grid) return hipSuccess;
+  const int64_t grid = (int64_t)device_cus() * std::min(per_cu, GroupShape<CT, D>::kPerCu);
+  if (grid <= 0 || items < 2 * (int64_t)device_cus()) return hipSuccess;
   *launched = true;
   hipLaunchKernelGGL((paged_decode_group_kernel<QT, CT, D, BS, S, NW, NB>), dim3((unsigned)grid), dim3(NT), 0, stream,
                      p);
