@@ -682,10 +682,13 @@ __device__ __forceinline__ void load_tile_rows_buf(Tile<D>& t, __amdgpu_buffer_r
   }
 }
 
-// Turns the V rows load_tile_rows left in t.v into the PV operand.
-// Whole-row V (RowsWhole): the raw words of token 4g + e, dimensions
-// (2m, 2m + 1) of the lane's n*NDL .. run, go to word e*W + m of t.v
-// (W = NDL / 2 words per token); transpose_tile_rows regroups them.
+// Whole-row V (RowsWhole, head sizes that are multiples of 32): lane (g, n)
+// loads dimensions n*NDL .. n*NDL + NDL - 1 (NDL = D / 16) of tokens 4g ..
+// 4g+3, so one load instruction of a quarter-wave covers a token's whole
+// row.  Word m of token 4g + e (dimensions n*NDL + 2m, +1) goes to word
+// e*W + m of t.v (W = NDL / 2 words per token; set_raw / raw_at address
+// t.v as 32-bit words), and transpose_tile_rows regroups the words into the
+// PV operand tiles 2m and 2m + 1.
 template <int D> __device__ __forceinline__ void set_raw(Tile<D>& t, int i, uint32_t w) {
   if (i & 1)
     t.v[i >> 1].y = w;
