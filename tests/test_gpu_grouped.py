@@ -187,6 +187,18 @@ def test_fp8_query_types_head_sizes(q_dtype, D, bs):
     check_fp8(fp8_radix_case(6900 + D + bs, D=D, bs=bs, q_dtype=q_dtype))
 
 
+@pytest.mark.parametrize("width", [256, 257])
+def test_fp8_group_context_bound(width):
+    # FP8 tables 4096 tokens wide (256 blocks of 16) still take the grouped
+    # kernel's FP8 shape (two workgroups of four wavefronts per CU, at most
+    # 4096 tokens); one block wider falls back to the one-sequence kernel.
+    # Both match the oracle.
+    c = fp8_radix_case(7100 + width, D=128, bs=16, q_dtype="bfloat16")
+    pad = width - c["bt"].shape[1]
+    c["bt"] = np.concatenate([c["bt"], np.full((c["bt"].shape[0], pad), -1, np.int32)], axis=1)
+    check_fp8(c)
+
+
 def test_fp8_empty_overlong_and_masked():
     c = fp8_radix_case(7000, D=64, bs=16, q_dtype="float16", prefix_tokens=128, suffix_hi=100)
     c["ctx"][[3, 77, 200]] = 0
