@@ -1919,11 +1919,11 @@ __global__ __launch_bounds__(64 * (Persist<D, BS == 0>::kWaves)) void paged_deco
 }
 
 // ---------------------------------------------------------------------------
-// Grouped persistent kernel (paged layout): each item is (S sequences of
-// neighbouring rank, KV head), and the 16 MFMA columns hold the GQA query
-// heads of all S sequences (S * group <= 16).  A wavefront walks its tiles
-// w, w+NW, ... of the longest of the S contexts (in the order described at
-// Job below); tile by tile:
+// Grouped persistent kernel (paged layout): each item is (S sequences whose
+// longest-first ranks are ngroups apart, KV head), and the 16 MFMA columns
+// hold the GQA query heads of all S sequences (S * group <= 16).  A
+// wavefront walks its tiles w, w+NW, ... of the longest of the S contexts (in
+// the order described at Job below); tile by tile:
 //   * shared -- every live sequence of the item maps the tile to the same
 //     block(s) and holds all 16 of its tokens: the tile is loaded once and
 //     feeds all columns (a radix-shared prefix is read once per S sequences);
@@ -1933,8 +1933,9 @@ __global__ __launch_bounds__(64 * (Persist<D, BS == 0>::kWaves)) void paged_deco
 // before the current one is consumed, so shared and private tiles follow
 // each other without a pipeline refill.  A tile is never loaded more often
 // than by the one-sequence kernels, and the MFMA count per loaded tile is the
-// same; what sharing saves is loads.  Items are ranked and dealt like the
-// persistent kernel's (groups of S sequences in longest-first order).
+// same; what sharing saves is loads.  Items are dealt like the persistent
+// kernel's (snake order over the workgroups); the sequences of an item are
+// taken S-strided from the longest-first order.
 // ---------------------------------------------------------------------------
 #ifndef PKV_GROUP_MAXSEQ
 #define PKV_GROUP_MAXSEQ 8192
@@ -2049,7 +2050,11 @@ __global__ __launch_bounds__(64 * NW, NW >= 8 ? 1 : 2) void paged_decode_group_k
     it.kvh = rank - gr * p.num_kv_heads;
 #pragma unroll
     for (int i = 0; i < S; ++i) {
-      const int sr = gr * S + i;
+      // Ranks gr, gr + ngroups, ...: every item mixes long and short
+      // contexts, so items are of like size and the snake order pairs them
+      // evenly (89.6 against 90.3 us with ranks gr*S .. gr*S + S-1 on the
+      // radix-shared B256 workload, mean of five same-process pairs).
+      const int sr = gr + i * ngroups;
       it.seq[i] = sr < B ? (ordered ? s_order[sr] : sr) : -1;
       const uint32_t c = it.seq[i] >= 0 ? (uint32_t)p.context_lens[it.seq[i]] : 0u;
       it.ctx[i] = (c != 0 && c <= (uint32_t)p.max_seq_len) ? c : 0u;
