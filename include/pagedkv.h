@@ -138,11 +138,12 @@ size_t pkv_paged_attention_workspace_size(int32_t num_seqs, int32_t num_heads,
  * Launches (all on `stream`): for partition_size = 0, contexts of at most
  * 16384 tokens and at least one (sequence, KV head) item per resident
  * workgroup, one persistent kernel that gives each item to one workgroup,
- * longest contexts first (with two or more items per workgroup, GQA groups
- * of at most 4 and contexts of at most 8192 tokens, items of four
- * sequences that share the MFMA columns, so that tiles the four map to the
- * same block are read once); otherwise a partition kernel, plus a
- * log-sum-exp merge kernel when a sequence has more than one partition.
+ * longest contexts first (with two or more items per CU, GQA groups of at
+ * most 4 and contexts of at most 8192 tokens -- 4096 over FP8 caches at
+ * head sizes 64 and 128 -- items of four sequences that share the MFMA
+ * columns, so that tiles the four map to the same block are read once);
+ * otherwise a partition kernel, plus a log-sum-exp merge kernel when a
+ * sequence has more than one partition.
  * query   : [num_seqs, num_heads, head_size], row stride q_stride.
  * out     : [num_seqs, num_heads, head_size] contiguous, same dtype as
  *           query, 16-byte aligned.
