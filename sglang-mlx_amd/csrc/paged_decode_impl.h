@@ -85,27 +85,19 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 // below 2^8, and the rescale of the accumulators is skipped for almost every
 // tile.  Any reference maximum gives the same normalised result.
 constexpr float kRescaleSlack = 8.f;
-#ifndef PKV_INPLACE_RESCALE
-#define PKV_INPLACE_RESCALE 1
-#endif
 
-#ifndef PKV_NBUF
-#define PKV_NBUF 4
-#endif
-#ifndef PKV_PAD_ZERO
-#define PKV_PAD_ZERO 1
-#endif
-#ifndef PKV_PART_NBUF
-#define PKV_PART_NBUF 2
-#endif
-// The one-sequence persistent kernel is used from PKV_PERSIST_MIN4 / 4
-// (sequence, unit) items per resident workgroup: from one item each, where
-// the longest-first order gives the longest items a workgroup of their own.
-// (From two, the Llama-3-8B layer at 48 and 63 sequences fell to the
-// partition kernel: 97.3 and 109.2 us against 76.6 and 95.9 us persistent.)
-#ifndef PKV_PERSIST_MIN4
-#define PKV_PERSIST_MIN4 4
-#endif
+// Tile buffers per wavefront where the register budget allows four (see
+// Prefetch), and of the partition kernel (two: fewer registers, more
+// resident workgroups per CU, measured 1-4% faster than three or four at
+// 32K-128K contexts).
+constexpr int kMaxBuffers = 4;
+constexpr int kPartBuffers = 2;
+// The one-sequence persistent kernel is used from one (sequence, unit) item
+// per resident workgroup, where the longest-first order gives the longest
+// items a workgroup of their own.  (From two, the Llama-3-8B layer at 48 and
+// 63 sequences fell to the partition kernel: 97.3 and 109.2 us against 76.6
+// and 95.9 us persistent.)
+constexpr int kPersistMinItemsPerWorkgroup = 1;
 
 // Query element pair -> (hi, lo) words of the cache type; q = hi + lo to
 // within 2^-16 relative, so a float32 query keeps its precision through the
@@ -170,7 +162,7 @@ template <bool WIDE> __device__ __forceinline__ constexpr int kstep_dim0(int j, 
 template <class QT, int D, int BS> struct Prefetch {
   static constexpr bool kF32 = std::is_same<QT, F32>::value;
   static constexpr bool kTight = kF32 || BS < kTile || D == 120;
-  static constexpr int kBuffers = (D > 128 || (kF32 && BS < kTile && D >= 120)) ? 2 : kTight ? 3 : PKV_NBUF;
+  static constexpr int kBuffers = (D > 128 || (kF32 && BS < kTile && D >= 120)) ? 2 : kTight ? 3 : kMaxBuffers;
 };
 
 // Word 3 of a raw (stride 0) buffer resource on gfx9-family GPUs.
@@ -1039,7 +1031,6 @@ __device__ __forceinline__ void softmax_tile(const DecodeParams& p, f32x4 sacc, 
     const float m_new = fmaxf(acc.m_run, mt);
     const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(acc.m_run - m_new);
     acc.l_run *= alpha;
-#if PKV_INPLACE_RESCALE
     // In place (each register multiplied where it lives): as a plain
     // product the compiler copied all DT x 4 accumulators on the path that
     // skips the rescale, every tile.
@@ -1047,10 +1038,6 @@ __device__ __forceinline__ void softmax_tile(const DecodeParams& p, f32x4 sacc, 
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) asm("v_mul_f32 %0, %0, %1" : "+v"(acc.o[dt][r]) : "v"(alpha));
-#else
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) acc.o[dt] *= alpha;
-#endif
     acc.m_run = m_new;
   }
   const float m_use = acc.m_run == -INFINITY ? 0.f : acc.m_run;
@@ -1310,7 +1297,7 @@ __device__ __forceinline__ void stream_tiles(const DecodeParams& p, const typena
       const int k = (tile - first) / NW;
       int b0 = blk.get(k * PT);
       int b1 = PT == 2 ? blk.get(k * PT + 1) : b0;
-      if constexpr (BS >= kTile && PKV_PAD_ZERO) {
+      if constexpr (BS >= kTile) {
         if (pad) b0 = b1 = -1;
       }
       if constexpr (F8)
@@ -1591,9 +1578,7 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_part_kernel(DecodeParams
   using CS = typename Elem<CT>::storage;
   const CS* kbase = static_cast<const CS*>(p.k_cache) + (int64_t)kvh * p.k_head_stride;
   const CS* vbase = static_cast<const CS*>(p.v_cache) + (int64_t)kvh * p.v_head_stride;
-  // Two tile buffers: fewer registers, more resident workgroups per CU
-  // (measured 1-4% faster than three or four at 32K-128K contexts).
-  stream_tiles<QT, CT, D, BS, NW, MAXT, PKV_PART_NBUF>(p, kbase, vbase, blk, t0, t1, ctx, wave, g, col, qa, qb, slope,
+  stream_tiles<QT, CT, D, BS, NW, MAXT, kPartBuffers>(p, kbase, vbase, blk, t0, t1, ctx, wave, g, col, qa, qb, slope,
                                                       acc);
 
   float M, L;
@@ -1723,27 +1708,13 @@ __global__ __launch_bounds__(64 * kPartWaves) void paged_decode_rows_kernel(Deco
 // length, block ids and query are loaded at its start, after the previous
 // item's merge (the reason is given at the item loop).
 // ---------------------------------------------------------------------------
-#ifndef PKV_ROWS_WAVES
-#define PKV_ROWS_WAVES 8
-#endif
-#ifndef PKV_ROWS_NBUF
-#define PKV_ROWS_NBUF 2
-#endif
-#ifndef PKV_FP8_NBUF
-#define PKV_FP8_NBUF 2
-#endif
-#ifndef PKV_PAGED_WAVES
-#define PKV_PAGED_WAVES 8
-#endif
-#ifndef PKV_PAGED_NBUF
-#define PKV_PAGED_NBUF 2
-#endif
 template <int D, bool ROWS = false, bool F8 = false> struct Persist {
   // Wavefronts per workgroup: two per SIMD while the register budget allows
   // (head sizes up to 128), one above.
-  static constexpr int kWaves = D <= 128 ? (ROWS ? PKV_ROWS_WAVES : PKV_PAGED_WAVES) : 4;
-  // Tile buffers per wavefront.
-  static constexpr int kMaxBuf = ROWS ? PKV_ROWS_NBUF : F8 ? PKV_FP8_NBUF : PKV_PAGED_NBUF;
+  static constexpr int kWaves = D <= 128 ? 8 : 4;
+  // Tile buffers per wavefront (one tile in flight beyond the consumed one:
+  // with eight streaming wavefronts per CU, deeper rings measured no faster).
+  static constexpr int kMaxBuf = 2;
 };
 
 // Rank of each of the first n entries of s_keys (distinct keys; the array
@@ -1937,11 +1908,8 @@ __global__ __launch_bounds__(64 * (Persist<D, BS == 0>::kWaves)) void paged_deco
 // kernel's (snake order over the workgroups); the sequences of an item are
 // taken S-strided from the longest-first order.
 // ---------------------------------------------------------------------------
-#ifndef PKV_GROUP_MAXSEQ
-#define PKV_GROUP_MAXSEQ 8192
-#endif
-constexpr int kGroupSeqs = 4;                   // sequences per item
-constexpr int kGroupMaxSeq = PKV_GROUP_MAXSEQ;  // longest context (block ids in registers)
+constexpr int kGroupSeqs = 4;       // sequences per item
+constexpr int kGroupMaxSeq = 8192;  // longest context (block ids in registers)
 
 template <int S> struct GroupItem {
   int kvh;
@@ -1958,16 +1926,7 @@ template <int S> struct GroupItem {
 // did.  Counters then showed 271 VALU and 128 SALU instructions per job
 // against 82 and 48 per tile in the one-sequence kernel (same 12 MFMAs and
 // 12 loads), which the per-item job list below removes.
-#ifndef PKV_GROUP_WAVES
-#define PKV_GROUP_WAVES 8
-#endif
-#ifndef PKV_GROUP_NBUF
-#define PKV_GROUP_NBUF 2
-#endif
-// Workgroups launched per CU (at most what fits).
-#ifndef PKV_GROUP_PER_CU
-#define PKV_GROUP_PER_CU 1
-#endif
+constexpr int kGroupBuffers = 2;
 // FP8 caches: two workgroups of four wavefronts per CU (the same eight
 // wavefronts, two items in flight per CU, so one item's job-list build and
 // merge overlap the other's stream): 66.7 against 70.4 us on the
@@ -1976,22 +1935,14 @@ template <int S> struct GroupItem {
 // so do FP8 head sizes that are not multiples of 64 (they would spill).
 template <class CT, int D> struct GroupShape {
   static constexpr bool kPairs = std::is_same<CT, FP8>::value && D % 64 == 0;
-  static constexpr int kWaves = kPairs ? 4 : PKV_GROUP_WAVES;
-  static constexpr int kPerCu = kPairs ? 2 : PKV_GROUP_PER_CU;
+  static constexpr int kWaves = kPairs ? 4 : 8;
+  static constexpr int kPerCu = kPairs ? 2 : 1;
 };
 // Longest context of the grouped kernel with NW wavefronts: each wavefront
 // lists at most 64 tiles of an item (one per lane).
 template <int NW> constexpr int group_max_seq() {
   return kGroupMaxSeq < 64 * kTile * NW ? kGroupMaxSeq : 64 * kTile * NW;
 }
-// Cache policy of the grouped kernel's tile loads: 0 = nontemporal for
-// private tiles only, 1 = nontemporal for all, 2 = default for all.
-#ifndef PKV_GROUP_CPOL
-#define PKV_GROUP_CPOL 0
-#endif
-#ifndef PKV_GROUP_ONE_CONSUME
-#define PKV_GROUP_ONE_CONSUME 1
-#endif
 
 
 template <class QT, class CT, int D, int BS, int S, int NW, int NB>
@@ -2286,7 +2237,7 @@ __global__ __launch_bounds__(64 * NW, NW >= 8 ? 1 : 2) void paged_decode_group_k
       // the radix-shared B256 workload, same process.  FP8 tiles keep the
       // two paths: their masking comes after the dequantisation and costs
       // more than the moves (75.8 against 72.0 us).
-      if (PKV_GROUP_ONE_CONSUME && !F8) {
+      if constexpr (!F8) {
         consume_tile<QT, CT, D, BS, false, true, true>(p, t, tt0, t1, lane_ctx, g, col, qa, qb, slope, acc, on,
                                                        partial);
       } else if (j.ntok < kTile) {
@@ -2330,7 +2281,7 @@ __global__ __launch_bounds__(64 * NW, NW >= 8 ? 1 : 2) void paged_decode_group_k
           // Each branch issues its loads, waits and consumes: with the
           // loads alone in the branches the compiler saw a path with no loads
           // and waited for all of them (vmcnt(0)) before every tile.
-          if (PKV_GROUP_CPOL == 1 || (PKV_GROUP_CPOL == 0 && jb[sl].i >= 0)) {
+          if (jb[sl].i >= 0) {
             load_job(t[sl], jb[sl], std::true_type{});
             __builtin_amdgcn_s_waitcnt(kWaitAhead);
             consume_job(t[b], jb[b], acc);
@@ -2505,7 +2456,7 @@ template <class QT, class CT, int D, int BS>
 static hipError_t launch_grouped(const DecodeParams& p, hipStream_t stream, bool* launched) {
   *launched = false;
   constexpr int S = kGroupSeqs;
-  constexpr int NW = GroupShape<CT, D>::kWaves, NB = PKV_GROUP_NBUF;
+  constexpr int NW = GroupShape<CT, D>::kWaves, NB = kGroupBuffers;
   if (p.slices != 1 || p.group * S > 16 || p.max_seq_len > group_max_seq<NW>()) return hipSuccess;
   constexpr int NT = 64 * NW;
   static int per_cu = -1;
@@ -2554,7 +2505,7 @@ static hipError_t launch_persistent(const DecodeParams& p, hipStream_t stream, b
   // for correctness).
   const int64_t items = (int64_t)p.num_seqs * p.units;
   const int64_t grid = (int64_t)device_cus() * per_cu;
-  if (grid <= 0 || 4 * items < PKV_PERSIST_MIN4 * grid) return hipSuccess;
+  if (grid <= 0 || items < kPersistMinItemsPerWorkgroup * grid) return hipSuccess;
   *launched = true;
   hipLaunchKernelGGL((paged_decode_persist_kernel<QT, CT, D, BS>), dim3((unsigned)grid), dim3(NT), 0, stream, p);
   return hipGetLastError();

@@ -132,22 +132,11 @@ typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 // nontemporal source loads (each source row is read once) 6.29 us; two or
 // eight wavefronts per workgroup 6.62 / 6.60 us; two tokens per wavefront
 // 6.85 us; one wavefront per (token, head) 9.68 us.
-#ifndef PKV_RAC_TPW
-#define PKV_RAC_TPW 1  // tokens per wavefront
-#endif
-#ifndef PKV_RAC_WAVES
-#define PKV_RAC_WAVES 4  // wavefronts per workgroup
-#endif
-#ifndef PKV_RAC_NTLOAD
-#define PKV_RAC_NTLOAD 1  // nontemporal source loads
-#endif
-#ifndef PKV_RAC_PER_HEAD
-#define PKV_RAC_PER_HEAD 0  // one wavefront per (token, head)
-#endif
+constexpr int kRacWaves = 4;  // wavefronts (tokens) per workgroup
 
 template <class KT, class CT>
 __device__ __forceinline__ uint4 load_src16(const typename Elem<KT>::storage* src) {
-  if constexpr (PKV_RAC_NTLOAD && std::is_same<KT, CT>::value) {
+  if constexpr (std::is_same<KT, CT>::value) {
     return __builtin_bit_cast(uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(src)));
   } else {
     return load_vec16<KT, CT>(src);
@@ -155,13 +144,13 @@ __device__ __forceinline__ uint4 load_src16(const typename Elem<KT>::storage* sr
 }
 
 template <class KT, class CT, int NV>
-__global__ __launch_bounds__(64 * PKV_RAC_WAVES) void rac_token_major_wave_kernel(RacParams p) {
+__global__ __launch_bounds__(64 * kRacWaves) void rac_token_major_wave_kernel(RacParams p) {
   using KS = typename Elem<KT>::storage;
   using CS = typename Elem<CT>::storage;
   constexpr int VE = 16 / Elem<CT>::kBytes;  // elements per 16-byte cache vector
-  constexpr int TPW = PKV_RAC_TPW;
+  constexpr int TPW = 1;  // tokens per wavefront
   const int lane = threadIdx.x & 63;
-  const int tok0 = ((int)blockIdx.x * PKV_RAC_WAVES + (int)(threadIdx.x >> 6)) * TPW;
+  const int tok0 = ((int)blockIdx.x * kRacWaves + (int)(threadIdx.x >> 6)) * TPW;
   const int row = p.num_heads * p.head_size;
   const int nvec = row / VE;  // 64 * (NV/2) < nvec <= 64 * NV
   uint4 kx[TPW][NV], vx[TPW][NV];
@@ -197,37 +186,6 @@ __global__ __launch_bounds__(64 * PKV_RAC_WAVES) void rac_token_major_wave_kerne
         }
       }
     }
-  }
-}
-
-// ---- token-major layout: one wavefront per (token, head) ----------------------------
-// The per-(token, head) decomposition, kept for comparison with the one above:
-// lanes 0 .. D/VE-1 move the head's K vectors and the next D/VE lanes its V
-// vectors (32 of 64 lanes at D = 128 with 16-bit caches), same
-// load / barrier / nontemporal-store phases.
-template <class KT, class CT>
-__global__ __launch_bounds__(256) void rac_token_major_head_kernel(RacParams p) {
-  using KS = typename Elem<KT>::storage;
-  using CS = typename Elem<CT>::storage;
-  constexpr int VE = 16 / Elem<CT>::kBytes;
-  const int lane = threadIdx.x & 63;
-  const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  const bool live = wid < p.num_tokens * p.num_heads;
-  const int64_t tok = live ? wid / p.num_heads : 0;
-  const int head = live ? (int)(wid - tok * p.num_heads) : 0;
-  const int hv = p.head_size / VE;  // vectors per head
-  const bool is_v = lane >= hv;
-  const int i = is_v ? lane - hv : lane;
-  const bool ok = live && lane < 2 * hv;
-  const int32_t slot = live ? p.slot_mapping[tok] : -1;
-  const KS* src = static_cast<const KS*>(is_v ? p.value : p.key) + tok * (is_v ? p.value_stride : p.key_stride) +
-                  (int64_t)head * p.head_size + i * VE;
-  const uint4 x = ok ? load_src16<KT, CT>(src) : make_uint4(0, 0, 0, 0);
-  __syncthreads();
-  if (ok && slot >= 0 && (int64_t)slot < p.num_slots) {
-    CS* dst = static_cast<CS*>(is_v ? p.value_cache : p.key_cache) +
-              ((int64_t)slot * p.num_heads + head) * p.head_size + i * VE;
-    __builtin_nontemporal_store(__builtin_bit_cast(u32x4_t, x), reinterpret_cast<u32x4_t*>(dst));
   }
 }
 
@@ -350,20 +308,15 @@ static hipError_t launch_rac_typed(const RacParams& p, bool aligned, hipStream_t
     // The one-wavefront-per-token kernels index tokens with 32-bit ints
     // (a workgroup covers at most 64 tokens).
     const int nvec = (vec && p.num_tokens <= INT32_MAX - 64) ? row / VE : 0;
-    const int64_t per_wg = (int64_t)PKV_RAC_WAVES * PKV_RAC_TPW;
-    const dim3 wgrid((unsigned)((p.num_tokens + per_wg - 1) / per_wg));
-    if (PKV_RAC_PER_HEAD && vec && p.head_size / VE <= 32) {
-      const int64_t waves = p.num_tokens * p.num_heads;
-      hipLaunchKernelGGL((rac_token_major_head_kernel<KT, CT>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream,
-                         p);
-    } else if (vec && nvec > 64 && nvec <= 128)
-      hipLaunchKernelGGL((rac_token_major_wave_kernel<KT, CT, 2>), wgrid, dim3(64 * PKV_RAC_WAVES), 0, stream, p);
+    const dim3 wgrid((unsigned)((p.num_tokens + kRacWaves - 1) / kRacWaves));
+    if (vec && nvec > 64 && nvec <= 128)
+      hipLaunchKernelGGL((rac_token_major_wave_kernel<KT, CT, 2>), wgrid, dim3(64 * kRacWaves), 0, stream, p);
     else if (vec && nvec > 128 && nvec <= 256)
-      hipLaunchKernelGGL((rac_token_major_wave_kernel<KT, CT, 4>), wgrid, dim3(64 * PKV_RAC_WAVES), 0, stream, p);
+      hipLaunchKernelGGL((rac_token_major_wave_kernel<KT, CT, 4>), wgrid, dim3(64 * kRacWaves), 0, stream, p);
     else if (vec && nvec > 256 && nvec <= 512)
-      hipLaunchKernelGGL((rac_token_major_wave_kernel<KT, CT, 8>), wgrid, dim3(64 * PKV_RAC_WAVES), 0, stream, p);
+      hipLaunchKernelGGL((rac_token_major_wave_kernel<KT, CT, 8>), wgrid, dim3(64 * kRacWaves), 0, stream, p);
     else if (vec && nvec > 512 && nvec <= 1024)
-      hipLaunchKernelGGL((rac_token_major_wave_kernel<KT, CT, 16>), wgrid, dim3(64 * PKV_RAC_WAVES), 0, stream, p);
+      hipLaunchKernelGGL((rac_token_major_wave_kernel<KT, CT, 16>), wgrid, dim3(64 * kRacWaves), 0, stream, p);
     else if (vec)
       hipLaunchKernelGGL((rac_token_major_kernel<KT, CT, VE, true>), grid, dim3(threads), 0, stream, p);
     else
