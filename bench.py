@@ -484,34 +484,47 @@ def bench_radix(dev, kernels, steps: int = 40, warmup: int = 5, layers: int = 4,
     from pkv_workloads import B, BS, D, HKV, HQ, SHARED_BLOCKS, RadixSharedWorkload
 
     w = RadixSharedWorkload(dev, kernels, layers=layers, fp8=fp8)
-    times = []
+    times = {"cascade": [], "v1": []}
     for it in range(warmup + steps):
         info = w.churn()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        queue_ahead()
-        a.record()
-        for layer in range(layers):
-            w.decode(layer, info["bt_dev"], info["ctx_dev"])
-        b.record()
-        if it >= warmup:
-            times.append((a, b))
+        for mode in ("cascade", "v1"):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            queue_ahead()
+            a.record()
+            for layer in range(layers):
+                if mode == "cascade":
+                    w.decode_cascade(layer, info["bt_dev"], info["ctx_dev"], info["plan"])
+                else:
+                    w.decode(layer, info["bt_dev"], info["ctx_dev"])
+            b.record()
+            if it >= warmup:
+                times[mode].append((a, b))
     torch.cuda.synchronize()
-    us = sorted(a.elapsed_time(b) * 1e3 / layers for a, b in times)
-    med = us[len(us) // 2]
+    meds = {}
+    for mode, ev in times.items():
+        us = sorted(a.elapsed_time(b) * 1e3 / layers for a, b in ev)
+        meds[mode] = us[len(us) // 2]
+    med = meds["cascade"]
     ctx_np = np.array([t.num_tokens for t in w.tables], dtype=np.int64)
     s_kv = 1 if fp8 else 2
     logical = decode_bytes(ctx_np, B, HQ, HKV, D, BS, s_kv=s_kv)
     unique = logical - (B - 1) * SHARED_BLOCKS * BS * HKV * D * 2 * s_kv
     cache = "FP8 E4M3 caches (k_scale 0.05, v_scale 0.02), bf16 query" if fp8 else "bf16"
+    v1 = meds["v1"]
     return dict(workload="radix-shared decode: B256, 32 q / 8 kv heads, D128, bs16, " + cache + ", 128 shared "
                          "blocks (2048 tokens) + U[64,512] private tokens, 10% private-block evict/realloc churn "
                          "per step (blocks change hands)",
+                path="paged_attention_cascade (prefix pass + tail pass, plan built on the host from the churned "
+                     "tables)",
                 us_per_launch=round(med, 2), unique_bytes_per_launch=int(unique), logical_bytes_per_launch=int(logical),
                 unique_gbs=round(unique / (med * 1e-6) / 1e9, 1),
                 unique_frac=round(unique / (med * 1e-6) / 1e9 / PEAK_GBS, 4),
                 effective_gbs=round(logical / (med * 1e-6) / 1e9, 1), kv_pools_rotated=layers,
-                method=(f"median over {steps} steps of a HIP event pair around {layers} back-to-back decode launches "
-                        f"(one per layer pool), divided by {layers}; churn and append outside"))
+                v1=dict(path="paged_attention_v1 (grouped persistent kernel, no plan)", us_per_launch=round(v1, 2),
+                        unique_frac=round(unique / (v1 * 1e-6) / 1e9 / PEAK_GBS, 4)),
+                method=(f"median over {steps} steps of a HIP event pair around {layers} back-to-back decode calls "
+                        f"(one per layer pool), divided by {layers}; churn, append and the plan's host build outside; "
+                        f"cascade and v1 timed alternately on the same steps"))
 
 
 def bench_cpu(res, budget_s):

@@ -197,6 +197,98 @@ int pkv_paged_attention(void* out, const void* query, const void* key_cache,
                         float k_scale, float v_scale, void* stream);
 
 /*
+ * Shared-prefix plan of pkv_paged_attention_cascade, built on the host from
+ * the block tables (sglang_mlx_amd.srt.mem_cache.build_cascade_plan).  All
+ * arrays are int32 device buffers.
+ *   prefix_lens [num_seqs]: leading tokens of each sequence that the prefix
+ *                pass covers, 0 for none; a multiple of block_size and of 16
+ *                (of 8 for 8-token blocks), at most the sequence's context.
+ *   order       [num_seqs]: the sequences by descending tail length
+ *                (context - prefix), a permutation of 0 .. num_seqs-1; it
+ *                only schedules the tail pass.
+ *   members     [num_members]: sequence ids, each prefix group's members
+ *                adjacent.
+ *   tiles       [num_tiles][4] (16-byte aligned): (member_begin,
+ *                member_count, token_begin, token_end) of one prefix-pass
+ *                unit.  members[member_begin .. +member_count) map tokens
+ *                [0, token_end) to the same blocks as the first of them and
+ *                have prefix_lens >= token_end; member_count * (num_heads /
+ *                num_kv_heads) <= 128; token_begin is a multiple of
+ *                chunk_tokens and token_end - token_begin <= chunk_tokens.
+ *                The units of a group cover its prefix [0, prefix_len)
+ *                chunk by chunk, and every member sits in the units of its
+ *                group.
+ *   chunk_tokens: a multiple of 16 and of block_size, at most 4096.
+ *   max_chunks  : at least ceil(prefix_lens[s] / chunk_tokens) for every s.
+ *   max_tail    : the longest context - prefix_lens[s] over the sequences.
+ * A plan that breaks these rules never makes a kernel read or write outside
+ * its buffers, but the rows it concerns are then undefined.
+ */
+typedef struct pkv_cascade_plan {
+  const int32_t* prefix_lens;
+  const int32_t* order;
+  const int32_t* members;
+  const int32_t* tiles;
+  int32_t num_members;
+  int32_t num_tiles;
+  int32_t chunk_tokens;
+  int32_t max_chunks;
+  int32_t max_tail;
+} pkv_cascade_plan;
+
+/*
+ * Workspace bytes of pkv_paged_attention_cascade: the larger of the one-pass
+ * decode's (pkv_paged_attention_workspace_size with partition_size 0) and
+ * the partial states' (num_seqs * num_heads * (max_chunks + 1) *
+ * (head_size + 2) float32, in four parts each 256-byte aligned).  Returns 0
+ * for invalid sizes.
+ */
+size_t pkv_paged_attention_cascade_workspace_size(int32_t num_seqs,
+                                                  int32_t num_heads,
+                                                  int32_t num_kv_heads,
+                                                  int32_t head_size,
+                                                  int32_t max_seq_len,
+                                                  int32_t max_chunks);
+
+/*
+ * Decode attention with radix-shared prefixes computed once per group
+ * (cascade).  No counterpart in the reference, whose radix cache shares
+ * token slots but whose kernel reads every sequence's context in full
+ * (paged_attention_kernels.metal:37-168); the result is
+ * pkv_paged_attention's with partition_size 0 (paged_attention_v1), to
+ * within floating-point rounding, for any plan that follows the rules of
+ * pkv_cascade_plan.  Arguments as pkv_paged_attention, PAGED5D layout.
+ * Launches on `stream`: a prefix pass (one workgroup per (plan tile, KV
+ * head): the tile's query rows against one chunk of the shared prefix, K/V
+ * staged through LDS, partial softmax states to the workspace), then a tail
+ * pass (one wavefront per (sequence, KV head): the prefix partials folded
+ * in, the tokens after the prefix streamed, the output row written).  The
+ * cascade kernels take 16-bit queries over caches of the same type or FP8
+ * (FP8 with blocks of 16 and 32 tokens), head sizes 64 and 128, GQA groups
+ * of at most 16, max_tail up to 2048 and
+ * V rows aligned for 16-byte loads; other shapes run the one-pass decode of
+ * pkv_paged_attention (the plan is then unused).
+ */
+int pkv_paged_attention_cascade(void* out, const void* query,
+                                const void* key_cache,
+                                const void* value_cache,
+                                const int32_t* block_tables,
+                                const int32_t* context_lens,
+                                const float* alibi_slopes,
+                                const pkv_cascade_plan* plan,
+                                int32_t num_seqs, int32_t num_heads,
+                                int32_t num_kv_heads, int32_t head_size,
+                                int32_t block_size,
+                                int32_t max_num_blocks_per_seq,
+                                int32_t max_seq_len, int64_t num_blocks,
+                                float scale, int64_t q_stride,
+                                int64_t k_block_stride, int64_t k_head_stride,
+                                int64_t v_block_stride, int64_t v_head_stride,
+                                void* workspace, size_t workspace_bytes,
+                                int32_t q_dtype, int32_t cache_dtype,
+                                float k_scale, float v_scale, void* stream);
+
+/*
  * Block-table decode attention that allocates nothing and takes no
  * workspace.  No counterpart in the reference: it is for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,

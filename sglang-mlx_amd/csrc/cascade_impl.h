@@ -1,0 +1,739 @@
+// Shared-prefix (cascade) decode attention for gfx950, paged 5-D layout.
+//
+// Semantics are those of paged_attention_v1 (paged_attention_kernels.metal:
+// 37-168 of the reference): per (sequence, query head), softmax over the
+// first ctx tokens of scale * q.k (+ alibi), weighted sum of V, denominator
+// sum + 1e-6, zero rows for ctx == 0 or ctx > max_seq_len.  The cascade only
+// changes where the work is done.  Sequences whose block tables begin with
+// the same blocks (a radix-shared prefix) are listed by the host in a plan
+// (CascadeParams), and two launches run:
+//
+// paged_cascade_kernel -- workgroups of 4 wavefronts in two roles, sized so
+//   that one of each shares a CU (LDS below half a CU's, at most 256 VGPRs
+//   per wavefront): the compute-bound prefix work and the HBM-bound tail
+//   work overlap.
+//   * Prefix role (workgroups 0 .. plan tiles x KV heads - 1): one plan
+//     tile's query rows (members x GQA heads, up to 128; each wavefront 32
+//     rows as two 16-column MFMA query sets held in registers) against one
+//     chunk of the group's prefix.  The chunk's K and V are staged through
+//     LDS two tiles of 16 tokens at a time (three buffers, two stages in
+//     flight) by direct-to-LDS buffer loads, in the order the MFMA operands
+//     want; every K/V byte is read from HBM (or L2) once per workgroup and
+//     from LDS once per wavefront, and feeds 32 query rows there.  FP8 codes
+//     are dequantised as they leave LDS.  Scores S^T = K Q^T and O^T += V^T P^T
+//     on v_mfma_f32_16x16x32 over tile pairs, online softmax in the log2
+//     domain; each row's partial state (max, sum, unnormalised output) goes
+//     to the workspace slot of its (sequence, head, chunk).
+//   * Tail role (the rest): one wavefront per (sequence, KV head) item,
+//     longest tail first: the tokens after the prefix (the sequence's private
+//     tail) through the one-sequence tile pipeline.  A sequence with no
+//     prefix gets its output row written here; otherwise the tail's partial
+//     state goes to the workspace.
+// paged_cascade_merge_kernel -- one wavefront per (sequence, KV head) with a
+//   prefix: the tail state and the chunks' partial states merged by
+//   log-sum-exp, the output row written.
+//
+// The log-sum-exp merge of partial states is an identity with one softmax
+// over all tokens (the final denominator is taken against the true maximum,
+// as the reference's), so the cascade returns paged_attention_v1's result
+// within floating-point rounding.
+#pragma once
+
+#include "paged_decode_impl.h"
+
+namespace pkv {
+
+constexpr int kCascadeWaves = 4;                               // wavefronts per workgroup, both roles
+constexpr int kPrefixSets = 2;                                 // 16-column query sets per wavefront
+constexpr int kPrefixRows = kCascadeWaves * kPrefixSets * 16;  // query rows per prefix workgroup
+constexpr int kPrefixStageTiles = 2;                           // 16-token tiles per LDS stage (one pair)
+constexpr int kPrefixBuffers = 3;                              // LDS stage buffers
+constexpr int kTailBuffers = 4;                                // tile buffers per tail wavefront
+constexpr int kMergeItemsPerWorkgroup = 4;
+
+// Largest block-table span of one prefix chunk (8-token blocks).
+constexpr int kPrefixMaxBlocks = kMaxPrefixChunk / 8;
+
+// LDS image of one staged 16-token tile, in 16-byte units.
+//   16-bit caches: K unit c8 * 16 + t = dimensions 8 c8 .. +7 of token t;
+//                  V unit 2d + h     = tokens 8h .. 8h+7 of dimension d.
+//   FP8 caches (codes): K unit c16 * 16 + t = dimensions 16 c16 .. +15 of
+//                  token t; V unit d = tokens 0 .. 15 of dimension d.
+// Every 64 consecutive units come from one (block, head) region of the
+// cache (one block with blocks of 16 and more; a half tile's block, by lane,
+// with 8-token blocks), so a wavefront stages a tile with direct-to-LDS
+// buffer loads, lane l of a load writing unit l of its 64.
+template <class CT, int D> struct PrefixTile {
+  static constexpr bool kF8 = std::is_same<CT, FP8>::value;
+  static constexpr int kKUnits = kF8 ? D : 2 * D;
+  static constexpr int kVUnits = kF8 ? D : 2 * D;
+  static constexpr int kUnits = kKUnits + kVUnits;
+  static_assert(kKUnits % 64 == 0 && kVUnits % 64 == 0, "whole 64-unit loads");
+};
+
+// A lane's MFMA operands of a staged tile pair (A, B) (16-bit caches as
+// loaded; FP8 codes dequantised exactly into MT):
+//   ka / kb[j]: K operand of k-step j (token col, dimensions 32j + 8g .. +7);
+//   v[dt]:      the PV operand of dimension tile dt over the pair's 32
+//               tokens, k-index 8g + e = token 4g + e of A (e < 4) and of B
+//               (e >= 4): dimension 16dt + col.
+template <class CT, class MT, int D> struct PrefixOperands {
+  uint4 ka[Tile<D>::KSTEPS], kb[Tile<D>::KSTEPS];
+  uint4 v[Tile<D>::DT];
+};
+
+template <class CT, class MT, int D>
+__device__ __forceinline__ void read_pair(PrefixOperands<CT, MT, D>& op, const uint4* ta, const uint4* tb, int lane,
+                                          int g, int col) {
+  using PT = PrefixTile<CT, D>;
+  constexpr int KSTEPS = Tile<D>::KSTEPS, DT = Tile<D>::DT;
+  if constexpr (!PT::kF8) {
+#pragma unroll
+    for (int j = 0; j < KSTEPS; ++j) {
+      op.ka[j] = ta[64 * j + lane];
+      op.kb[j] = tb[64 * j + lane];
+    }
+    const char* va = reinterpret_cast<const char*>(ta + PT::kKUnits);
+    const char* vb = reinterpret_cast<const char*>(tb + PT::kKUnits);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const int o = (16 * dt + col) * 32 + 8 * g;
+      const uint2 x = *reinterpret_cast<const uint2*>(va + o), y = *reinterpret_cast<const uint2*>(vb + o);
+      op.v[dt] = make_uint4(x.x, x.y, y.x, y.y);
+    }
+  } else {
+    uint2 ka8[KSTEPS], kb8[KSTEPS];
+    uint32_t va8[DT], vb8[DT];
+    const char* ka_ = reinterpret_cast<const char*>(ta);
+    const char* kb_ = reinterpret_cast<const char*>(tb);
+#pragma unroll
+    for (int j = 0; j < KSTEPS; ++j) {
+      const int o = ((2 * j + (g >> 1)) * 16 + col) * 16 + (g & 1) * 8;
+      ka8[j] = *reinterpret_cast<const uint2*>(ka_ + o);
+      kb8[j] = *reinterpret_cast<const uint2*>(kb_ + o);
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const int o = PT::kKUnits * 16 + (16 * dt + col) * 16 + 4 * g;
+      va8[dt] = *reinterpret_cast<const uint32_t*>(ka_ + o);
+      vb8[dt] = *reinterpret_cast<const uint32_t*>(kb_ + o);
+    }
+    // Exponent-15 codes (the reference's inf / NaN) take the exact path;
+    // one wave-wide test for the pair.
+    uint32_t probe = 0;
+#pragma unroll
+    for (int j = 0; j < KSTEPS; ++j) probe |= fp8x4_special(ka8[j].x) | fp8x4_special(ka8[j].y) |
+                                              fp8x4_special(kb8[j].x) | fp8x4_special(kb8[j].y);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) probe |= fp8x4_special(va8[dt]) | fp8x4_special(vb8[dt]);
+    const bool special = __any(probe != 0u);
+    auto cvt = [&](uint32_t w) { return special ? fp8x4_exact<MT>(w) : fp8x4_cvt<MT>(w); };
+#pragma unroll
+    for (int j = 0; j < KSTEPS; ++j) {
+      uint2 lo = cvt(ka8[j].x), hi = cvt(ka8[j].y);
+      op.ka[j] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+      lo = cvt(kb8[j].x), hi = cvt(kb8[j].y);
+      op.kb[j] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const uint2 x = cvt(va8[dt]), y = cvt(vb8[dt]);
+      op.v[dt] = make_uint4(x.x, x.y, y.x, y.y);
+    }
+  }
+}
+
+// Stages part PART (0: the K units, 1: the V units) of tokens tt0 ..
+// tt0+15 of the (block, head) regions at `base` into the LDS tile `dst`:
+// b0 is the block of tokens 0 .. 7 and b1 of 8 .. 15 (equal with blocks of
+// 16 and more; -1: outside the pool or past the chunk).  A block of -1 gets
+// a zero-sized buffer resource, so its units read as zeros.  Returns the
+// tile's live-token mask (bit i = token i).
+template <class CT, int D, int BS, int PART>
+__device__ __forceinline__ uint32_t stage_part(uint4* dst, const typename Elem<CT>::storage* base, int64_t block_stride,
+                                               int b0, int b1, int tt0, int lane) {
+  using PT = PrefixTile<CT, D>;
+  constexpr int EB = Elem<CT>::kBytes;
+  constexpr int REGION = D * BS * EB;  // bytes of one (block, head) region of K (and of V)
+  typedef __attribute__((address_space(3))) void* lds_ptr;
+  auto rsrc = [&](int b) __attribute__((always_inline)) {
+    return __builtin_amdgcn_make_buffer_rsrc((void*)(base + (int64_t)(b < 0 ? 0 : b) * block_stride), (short)0,
+                                             b < 0 ? 0 : REGION, kBufferRsrcWord3);
+  };
+  const int hi = lane >> 4, t = lane & 15;
+  uint4* out = dst + (PART == 0 ? 0 : PT::kKUnits);
+  constexpr int LOADS = (PART == 0 ? PT::kKUnits : PT::kVUnits) / 64;
+  if constexpr (BS >= kTile) {
+    const int off = tt0 % BS;
+    const __amdgpu_buffer_rsrc_t r = rsrc(b0);
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+      if constexpr (PART == 0)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)(out + 64 * j), 16, ((4 * j + hi) * BS + t) * 16, off * 16,
+                                                 0, 0);
+      else if constexpr (PT::kF8)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)(out + 64 * j), 16, (64 * j + lane) * BS, off, 0, 0);
+      else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr)(out + 64 * j), 16,
+                                                 ((32 * j + (lane >> 1)) * BS + 8 * (lane & 1)) * 2, off * 2, 0, 0);
+    }
+  } else {
+    static_assert(!PT::kF8, "FP8 caches with 8-token blocks are not staged");
+    // 8-token blocks: each load goes out twice, to the lanes of each half
+    // tile with that half's block.
+    const __amdgpu_buffer_rsrc_t r0 = rsrc(b0), r1 = rsrc(b1);
+    const bool first = PART == 0 ? t < 8 : (lane & 1) == 0;
+#pragma unroll
+    for (int j = 0; j < LOADS; ++j) {
+      const int vo = PART == 0 ? ((4 * j + hi) * BS + (t & 7)) * 16 : (32 * j + (lane >> 1)) * BS * 2;
+      if (first)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r0, (lds_ptr)(out + 64 * j), 16, vo, 0, 0, 0);
+      else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r1, (lds_ptr)(out + 64 * j), 16, vo, 0, 0, 0);
+    }
+  }
+  return (b0 >= 0 ? 0x00ffu : 0u) | (b1 >= 0 ? 0xff00u : 0u);
+}
+
+
+// Prefix role: plan tile `wi`, KV head `kvh` (see the file comment).
+template <class QT, class CT, int D, int BS>
+__device__ __forceinline__ void prefix_role(const DecodeParams& p, const CascadeParams& c, int wi, int kvh,
+                                            uint4 (*s_buf0)[PrefixTile<CT, D>::kUnits],
+                                            uint4 (*s_buf1)[PrefixTile<CT, D>::kUnits],
+                                            uint4 (*s_buf2)[PrefixTile<CT, D>::kUnits], int32_t* s_blk,
+                                            uint32_t (*s_live)[kPrefixStageTiles]) {
+  using MT = typename MmaOf<QT, CT>::type;
+  using CS = typename Elem<CT>::storage;
+  using PT = PrefixTile<CT, D>;
+  constexpr int NW = kCascadeWaves, NS = kPrefixSets, ST = kPrefixStageTiles;
+  constexpr int NT = 64 * NW;
+  constexpr int KSTEPS = Tile<D>::KSTEPS;
+  constexpr int DT = Tile<D>::DT;
+  static_assert(ST == 2 && NW == 2 * ST, "wavefront w stages part w % 2 of tile w / 2; one pair per stage");
+  static_assert(PT::kKUnits == PT::kVUnits, "K and V parts stage alike");
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, col = lane & 15;
+  const int4 e = c.tiles[wi];
+  const int mb = e.x, mc = e.y, t0 = e.z;
+  // A malformed tile (the host builds them) is skipped, never read past.
+  const int tcap = p.max_blocks_per_seq * BS;
+  const int t1 = min(e.w, tcap);
+  if (mb < 0 || mc <= 0 || mb > c.num_members - mc || mc * p.group > kPrefixRows || t0 < 0 || t0 >= t1 ||
+      t1 - t0 > c.chunk || t0 % c.chunk != 0 || t0 / c.chunk >= c.max_chunks)
+    return;
+  const int chunk_idx = t0 / c.chunk;
+  const int seq0 = c.members[mb];
+  if (seq0 < 0 || seq0 >= p.num_seqs) return;
+
+  // Block ids of the chunk (from the first member's table): -1 outside the
+  // pool.  Blocks only partly inside [t0, t1) count as outside: a chunk
+  // ends on a block boundary (the plan's prefixes are whole blocks).
+  const int lb0 = t0 / BS;
+  const int nlb = t1 / BS - lb0;
+  {
+    const int32_t* row = p.block_tables + (int64_t)seq0 * p.max_blocks_per_seq;
+    for (int i = tid; i < nlb; i += NT) {
+      const int b = row[lb0 + i];
+      s_blk[i] = (int64_t)(uint32_t)b < p.num_blocks ? b : -1;
+    }
+  }
+  // The lane's query rows: set s, row (wave * NS + s) * 16 + col = (member
+  // r / group, head kvh * group + r % group).
+  int seqs[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const int r = (wave * NS + s) * 16 + col;
+    const int m = r / p.group;
+    const int sq = m < mc ? c.members[mb + m] : -1;
+    seqs[s] = (sq >= 0 && sq < p.num_seqs) ? sq : -1;
+  }
+  __syncthreads();  // s_blk
+
+  const CS* kbase = static_cast<const CS*>(p.k_cache) + (int64_t)kvh * p.k_head_stride;
+  const CS* vbase = static_cast<const CS*>(p.v_cache) + (int64_t)kvh * p.v_head_stride;
+  const int ntiles = (t1 - t0 + kTile - 1) / kTile;
+  const int nstages = (ntiles + ST - 1) / ST;
+  auto buffer = [&](auto k) __attribute__((always_inline)) -> uint4 (*)[PT::kUnits] {
+    if constexpr (decltype(k)::value == 0) return s_buf0;
+    else if constexpr (decltype(k)::value == 1) return s_buf1;
+    else return s_buf2;
+  };
+  // Wavefront w stages part w % 2 (K, V) of tile w / 2 of a stage.
+  const int my_tile = wave >> 1, my_part = wave & 1;
+  auto stage = [&](auto k, int st) __attribute__((always_inline)) {
+    const int tt0 = t0 + (st * ST + my_tile) * kTile;
+    auto blk_of = [&](int tok) __attribute__((always_inline)) {
+      const int lb = tok / BS - lb0;
+      return (tok < t1 && lb < nlb) ? __builtin_amdgcn_readfirstlane(s_blk[lb]) : -1;
+    };
+    const int b0 = blk_of(tt0);
+    const int b1 = BS >= kTile ? b0 : blk_of(tt0 + 8);
+    uint4* dst = buffer(k)[my_tile];
+    if (my_part == 0) {
+      const uint32_t live = stage_part<CT, D, BS, 0>(dst, kbase, p.k_block_stride, b0, b1, tt0, lane);
+      if (lane == 0) s_live[decltype(k)::value][my_tile] = live;
+    } else {
+      stage_part<CT, D, BS, 1>(dst, vbase, p.v_block_stride, b0, b1, tt0, lane);
+    }
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  static_assert(kPrefixBuffers == 3, "three stage buffers");
+  stage(I0{}, 0);
+  if (1 < nstages) stage(I1{}, 1);
+
+  // Scores are scale * q.k in the log2 domain.  A negative scale is folded
+  // into the query's sign bits (exact), so the softmax sees scale >= 0 and
+  // the largest raw score is the largest scaled one.
+  const float cs = fabsf(p.scale_log2);
+  const uint32_t qsign = p.scale_log2 < 0.f ? 0x80008000u : 0u;
+  uint4 qa[NS][KSTEPS];
+  uint4 qdummy[1];
+  int lim[NS], ctxs[NS];
+  int64_t slot[NS];
+  float slope[NS];
+  bool on[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const int r = (wave * NS + s) * 16 + col;
+    const int head = kvh * p.group + (r % p.group);
+    const int seq = seqs[s];
+    const uint32_t ctx = (uint32_t)p.context_lens[seq < 0 ? 0 : seq];
+    const bool live = seq >= 0 && ctx != 0 && ctx <= (uint32_t)p.max_seq_len;
+    on[s] = live;
+    ctxs[s] = live ? (int)ctx : 0;
+    lim[s] = live ? min((int)ctx, t1) : t0;
+    slot[s] = live ? (((int64_t)seq * p.num_heads + head) * c.max_chunks + chunk_idx) : 0;
+    load_query_lane<QT, MT, D, false>(p, seq, head, seq >= 0, g, qa[s], qdummy);
+#pragma unroll
+    for (int j = 0; j < KSTEPS; ++j)
+      qa[s][j] = make_uint4(qa[s][j].x ^ qsign, qa[s][j].y ^ qsign, qa[s][j].z ^ qsign, qa[s][j].w ^ qsign);
+    slope[s] = p.alibi != nullptr ? p.alibi[head] * kLog2e : 0.f;
+  }
+  // The plain softmax step (no ALiBi, scale > 0): max over raw scores,
+  // weights exp2(fma(s, scale, -m)); otherwise scaled scores first.
+  const bool plain = p.alibi == nullptr && cs > 0.f;
+
+  WaveAcc<D> acc[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) acc[s].init();
+
+  // One tile pair: scores of both tiles per query set, one online-softmax
+  // step over their 32 tokens, P V^T on 16x16x32 MFMAs.  Each phase runs
+  // for both query sets before the next, so that the two sets' dependent
+  // chains (MFMA results -> softmax -> MFMA operands) interleave.
+  auto consume_pair = [&](const uint4* ta, const uint4* tb, uint32_t live_a, uint32_t live_b,
+                          int tok_a) __attribute__((always_inline)) {
+    PrefixOperands<CT, MT, D> op;
+    read_pair<CT, MT, D>(op, ta, tb, lane, g, col);
+    const int va = tok_a + 4 * g, vb = va + kTile;
+    f32x4 sa[NS], sb[NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) sa[s] = sb[s] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < KSTEPS; ++j)
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        sa[s] = Mma<MT>::k32(op.ka[j], qa[s][j], sa[s]);
+        sb[s] = Mma<MT>::k32(op.kb[j], qa[s][j], sb[s]);
+      }
+    // Token liveness of the lane's 4 + 4 tokens; the context bound per set.
+    const uint32_t la = (live_a >> (4 * g)) & 15u, lb = (live_b >> (4 * g)) & 15u;
+    float sc[NS][8], mt[NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const bool whole = la == 15u && lb == 15u && vb + 3 < lim[s];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float xa = sa[s][r], xb = sb[s][r];
+        if (!plain) {
+          xa *= cs;
+          xb *= cs;
+          if (p.alibi != nullptr) {
+            xa += slope[s] * (float)(va + r - ctxs[s] + 1);
+            xb += slope[s] * (float)(vb + r - ctxs[s] + 1);
+          }
+        }
+        sc[s][r] = xa;
+        sc[s][4 + r] = xb;
+      }
+      if (!__all(whole)) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          sc[s][r] = (((la >> r) & 1u) && va + r < lim[s]) ? sc[s][r] : -INFINITY;
+          sc[s][4 + r] = (((lb >> r) & 1u) && vb + r < lim[s]) ? sc[s][4 + r] : -INFINITY;
+        }
+      }
+      mt[s] = fmaxf(fmaxf(fmaxf(sc[s][0], sc[s][1]), fmaxf(sc[s][2], sc[s][3])),
+                    fmaxf(fmaxf(sc[s][4], sc[s][5]), fmaxf(sc[s][6], sc[s][7])));
+    }
+#pragma unroll
+    for (int s = 0; s < NS; ++s) mt[s] = column_max(mt[s]) * (plain ? cs : 1.f);  // log2 units
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      WaveAcc<D>& a = acc[s];
+      a.m_max = fmaxf(a.m_max, mt[s]);
+      if (__any(mt[s] > a.m_run + kRescaleSlack)) {
+        const float m_new = fmaxf(a.m_run, mt[s]);
+        const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(a.m_run - m_new);
+        a.l_run *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) a.o[dt] *= alpha;
+        a.m_run = m_new;
+      }
+    }
+    uint4 pp[NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      WaveAcc<D>& a = acc[s];
+      const float m_use = a.m_run == -INFINITY ? 0.f : a.m_run;
+      const float cm = plain ? cs : 1.f;
+      float pr[8];
+#pragma unroll
+      for (int r = 0; r < 8; ++r) pr[r] = fast_exp2(__builtin_fmaf(sc[s][r], cm, -m_use));
+      a.l_run += ((pr[0] + pr[1]) + (pr[2] + pr[3])) + ((pr[4] + pr[5]) + (pr[6] + pr[7]));
+      pp[s] = make_uint4(pack_p<MT>(pr[0], pr[1]), pack_p<MT>(pr[2], pr[3]), pack_p<MT>(pr[4], pr[5]),
+                         pack_p<MT>(pr[6], pr[7]));
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int s = 0; s < NS; ++s) acc[s].o[dt] = Mma<MT>::k32(op.v[dt], pp[s], acc[s].o[dt]);
+  };
+  // Direct-to-LDS loads a wavefront issues per stage; s_waitcnt immediates
+  // (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt in 6:4 left at its
+  // maximum, lgkmcnt 0) that leave 0 or 1 later stage's loads in flight.
+  constexpr int LPS = PT::kKUnits / 64 * (BS >= kTile ? 1 : 2);
+  static_assert(LPS < 64, "vmcnt counts at most 63 loads");
+  constexpr int kWait0 = (7 << 4);
+  constexpr int kWait1 = (LPS & 15) | ((LPS >> 4) << 14) | (7 << 4);
+  // The workgroup meets at a bare s_barrier (a __syncthreads, or any
+  // workgroup fence that covers LDS, waits for every outstanding
+  // direct-to-LDS load, the stage in flight included).  Each wavefront
+  // first waits explicitly for its own loads of the next stage and its LDS
+  // writes (the kWait* immediates); the asm's memory clobber keeps the
+  // compiler from moving memory accesses across the barrier.
+  auto barrier = [] __attribute__((always_inline)) { asm volatile("s_barrier" ::: "memory"); };
+  __builtin_amdgcn_s_waitcnt(kWait0);  // stages 0 and 1, and the queries
+  barrier();
+  // Step k of a turn consumes stage st (buffer k), issues stage st + 2 into
+  // the buffer consumed one step earlier, waits for stage st + 1 and meets
+  // the workgroup at a barrier.
+  auto step = [&](auto k, int st) __attribute__((always_inline)) {
+    constexpr int K = decltype(k)::value;
+    if (st + 2 < nstages) stage(std::integral_constant<int, (K + 2) % 3>{}, st + 2);
+    consume_pair(buffer(k)[0], buffer(k)[1], s_live[K][0], s_live[K][1], t0 + st * ST * kTile);
+    if (st + 2 < nstages)
+      __builtin_amdgcn_s_waitcnt(kWait1);
+    else
+      __builtin_amdgcn_s_waitcnt(kWait0);
+    barrier();
+  };
+  for (int st = 0; st < nstages; st += 3) {
+    step(I0{}, st);
+    if (st + 1 >= nstages) break;
+    step(I1{}, st + 1);
+    if (st + 2 >= nstages) break;
+    step(I2{}, st + 2);
+  }
+
+  // Partial states: each row's true maximum, its weight sum against it and
+  // the unnormalised output.
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    WaveAcc<D>& a = acc[s];
+    if (a.m_max != -INFINITY && a.m_max != a.m_run) {
+      const float f = exp2f(a.m_run - a.m_max);
+      a.l_run *= f;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) a.o[dt] *= f;
+      a.m_run = a.m_max;
+    }
+    const float l_col = column_sum(a.l_run);
+    if (!on[s]) continue;
+    float* wo = c.ws_o + slot[s] * D;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+      *reinterpret_cast<float4*>(wo + 16 * dt + 4 * g) = make_float4(a.o[dt][0], a.o[dt][1], a.o[dt][2], a.o[dt][3]);
+    if (g == 0) *reinterpret_cast<float2*>(c.ws_ml + slot[s] * 2) = make_float2(a.m_max, l_col);
+  }
+}
+
+// Folds one partial state (maximum m, weight sum l against it, unnormalised
+// output o of the lane's dimensions) into acc, whose m_run is its true
+// maximum.  The sum goes to the g == 0 lane of each column only: acc.l_run
+// holds per-lane parts that are summed over the column at the end.
+template <int D>
+__device__ __forceinline__ void fold_partial(WaveAcc<D>& acc, float m, float l, const float4 (&o)[Tile<D>::DT],
+                                             int g) {
+  if (m == -INFINITY) return;
+  if (m > acc.m_run) {
+    const float f = acc.m_run == -INFINITY ? 0.f : exp2f(acc.m_run - m);
+    acc.l_run *= f;
+#pragma unroll
+    for (int dt = 0; dt < Tile<D>::DT; ++dt) acc.o[dt] *= f;
+    acc.m_run = m;
+  }
+  const float w = exp2f(m - acc.m_run);
+#pragma unroll
+  for (int dt = 0; dt < Tile<D>::DT; ++dt) {
+    acc.o[dt][0] += w * o[dt].x;
+    acc.o[dt][1] += w * o[dt].y;
+    acc.o[dt][2] += w * o[dt].z;
+    acc.o[dt][3] += w * o[dt].w;
+  }
+  if (g == 0) acc.l_run += w * l;
+  acc.m_max = acc.m_run;
+}
+
+// Folds the prefix partials of one item's heads into acc (columns col <
+// nh).  The chunks are spread over the wavefront's columns: column col takes
+// head col % nh of chunk c0 + col / nh, for as many chunks per pass as a
+// power of two of nh-column groups fits in 16, so each lane loads one
+// partial (its 4 x DT output values) and the combination runs as a tree of
+// lane exchanges (chunk c absorbs chunk c + s at step s).  row0: workspace
+// row of head 0 of the item, (seq * Hq + h0) * max_chunks.
+template <int D>
+__device__ __forceinline__ void fold_prefix(const CascadeParams& c, int64_t row0, int nh, int nch, int g, int col,
+                                            WaveAcc<D>& acc) {
+  constexpr int DT = Tile<D>::DT;
+  int per = 1;
+  while (per * 2 * nh <= 16) per *= 2;
+  const int h = col % nh, cl = col / nh;
+  const bool mine = cl < per;
+  for (int c0 = 0; c0 < nch; c0 += per) {
+    const int ch = c0 + cl;
+    const bool ok = mine && ch < nch;
+    const int64_t r = (row0 + (int64_t)h * c.max_chunks + (ok ? ch : 0));
+    const float2 ml = *reinterpret_cast<const float2*>(c.ws_ml + r * 2);
+    float4 o[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) o[dt] = *reinterpret_cast<const float4*>(c.ws_o + r * D + 16 * dt + 4 * g);
+    float m = ok ? ml.x : -INFINITY;
+    float l = ok ? ml.y : 0.f;
+    for (int st = 1; st < per; st *= 2) {
+      // Chunk cl absorbs chunk cl + st (lanes st * nh columns to the right).
+      const int src = (g << 4) + min(col + st * nh, 15);
+      const bool take = mine && (cl % (2 * st)) == 0 && cl + st < per;
+      const float pm = __shfl(m, src), pl = __shfl(l, src);
+      const float M = fmaxf(m, take ? pm : -INFINITY);
+      const float fa = (m == -INFINITY) ? 0.f : exp2f(m - M);
+      const float fb = (!take || pm == -INFINITY) ? 0.f : exp2f(pm - M);
+      l = l * fa + pl * fb;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const float4 po = make_float4(__shfl(o[dt].x, src), __shfl(o[dt].y, src), __shfl(o[dt].z, src),
+                                      __shfl(o[dt].w, src));
+        o[dt] = make_float4(o[dt].x * fa + po.x * fb, o[dt].y * fa + po.y * fb, o[dt].z * fa + po.z * fb,
+                            o[dt].w * fa + po.w * fb);
+      }
+      m = M;
+    }
+    if (col < nh) fold_partial<D>(acc, m, l, o, g);
+  }
+}
+
+
+// The prefix length a sequence's rows take from the plan: 0 when the
+// sequence is not live, has no prefix, or the plan's value cannot be used
+// (not a multiple of the tile alignment, or beyond the workspace's chunks);
+// the context is then streamed whole.  The tail and merge kernels decide
+// alike.
+template <int BS>
+__device__ __forceinline__ int usable_prefix(const CascadeParams& c, int seq, bool live) {
+  constexpr int ALIGN = BS < kTile ? BS : kTile;  // a tail starts on a tile boundary of its blocks
+  const int pre = live ? c.prefix_lens[seq] : 0;
+  return (pre < 0 || pre % ALIGN != 0 || pre > c.max_chunks * c.chunk) ? 0 : pre;
+}
+
+// Tail role: tail wavefront `tw` of `tws` takes items tw, tw + tws, ... of
+// the longest-tail-first order.
+template <class QT, class CT, int D, int BS>
+__device__ __forceinline__ void tail_role(const DecodeParams& p, const CascadeParams& c, int tw, int tws) {
+  using QS = typename Elem<QT>::storage;
+  using CS = typename Elem<CT>::storage;
+  using MT = typename MmaOf<QT, CT>::type;
+  constexpr int KSTEPS = Tile<D>::KSTEPS;
+  constexpr int DT = Tile<D>::DT;
+  constexpr int MAXT = kTailMaxTokens / kTile;
+  using Blocks = WaveBlocks<BS, MAXT>;
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4, col = lane & 15;
+  const int total = p.num_seqs * p.units;
+  for (int rank = tw; rank < total; rank += tws) {
+    const int sr = rank / p.units;
+    const int unit = rank - sr * p.units;
+    const int seq = c.order[sr];
+    if (seq < 0 || seq >= p.num_seqs) continue;  // malformed order: the rows are not written
+    int kvh, h0, nh;
+    unit_heads(p, unit, kvh, h0, nh);
+    const uint32_t ctx = (uint32_t)p.context_lens[seq];
+    const bool live = ctx != 0 && ctx <= (uint32_t)p.max_seq_len;
+    const int pre = usable_prefix<BS>(c, seq, live);
+    const int t0 = min(pre, (int)ctx);
+    const int t1 = min((int)ctx, t0 + kTailMaxTokens);
+
+    Blocks blk;
+    const int lb0 = t0 / BS;
+    blk.load(p.block_tables + (int64_t)seq * p.max_blocks_per_seq, p.num_blocks,
+             live ? (t1 + BS - 1) / BS - lb0 : 0, lb0, t0, 0, 1, lane);
+    uint4 qa[KSTEPS];
+    uint4 qb[1];
+    load_query<QT, MT, D, WideFp8<CT, D>::value>(p, seq, h0, nh, g, col, qa, qb);
+    const float slope = (p.alibi != nullptr && col < nh) ? p.alibi[h0 + col] * kLog2e : 0.f;
+
+    WaveAcc<D> acc;
+    acc.init();
+    if (live && t1 > t0) {
+      const CS* kbase = static_cast<const CS*>(p.k_cache) + (int64_t)kvh * p.k_head_stride;
+      const CS* vbase = static_cast<const CS*>(p.v_cache) + (int64_t)kvh * p.v_head_stride;
+      stream_tiles<QT, CT, D, BS, 1, MAXT, kTailBuffers>(p, kbase, vbase, blk, t0, t1, ctx, 0, g, col, qa, qb, slope,
+                                                         acc);
+    }
+    if (acc.m_max != -INFINITY && acc.m_max != acc.m_run) {
+      const float f = exp2f(acc.m_run - acc.m_max);
+      acc.l_run *= f;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) acc.o[dt] *= f;
+    }
+    const float L = column_sum(acc.l_run);
+    if (col >= nh) continue;
+    const int64_t row = (int64_t)seq * p.num_heads + h0 + col;
+    if (pre > 0) {
+      // The merge kernel finishes the row: the tail's state, as a partial.
+      float* wo = c.ws_tail_o + row * D;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+        *reinterpret_cast<float4*>(wo + 16 * dt + 4 * g) =
+            make_float4(acc.o[dt][0], acc.o[dt][1], acc.o[dt][2], acc.o[dt][3]);
+      if (g == 0) *reinterpret_cast<float2*>(c.ws_tail_ml + row * 2) = make_float2(acc.m_max, L);
+    } else {
+      const float inv = live ? p.v_scale / (L + 1e-6f) : 0.f;
+      QS* out = static_cast<QS*>(p.out) + row * D;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+        store4<QT>(out + 16 * dt + 4 * g, acc.o[dt][0] * inv, acc.o[dt][1] * inv, acc.o[dt][2] * inv,
+                   acc.o[dt][3] * inv);
+    }
+  }
+}
+
+// Prefix and tail roles in one launch (see the file comment).
+template <class QT, class CT, int D, int BS>
+__global__ __launch_bounds__(64 * kCascadeWaves, 2) void paged_cascade_kernel(DecodeParams p, CascadeParams c) {
+  using PT = PrefixTile<CT, D>;
+  static_assert(D % 64 == 0, "head sizes 64 and 128");
+  static_assert(!std::is_same<QT, F32>::value, "the cascade takes a 16-bit query");
+  __shared__ uint4 s_buf0[kPrefixStageTiles][PT::kUnits];
+  __shared__ uint4 s_buf1[kPrefixStageTiles][PT::kUnits];
+  __shared__ uint4 s_buf2[kPrefixStageTiles][PT::kUnits];
+  __shared__ int32_t s_blk[kPrefixMaxBlocks];
+  __shared__ uint32_t s_live[kPrefixBuffers][kPrefixStageTiles];
+  const int prefix_wgs = c.num_tiles * p.num_kv_heads;
+  if ((int)blockIdx.x < prefix_wgs) {
+    // The prefix role is compute-bound and sets the launch's length; its
+    // wavefronts take issue priority over the memory-bound tail wavefronts
+    // sharing their SIMDs.
+    __builtin_amdgcn_s_setprio(3);
+    prefix_role<QT, CT, D, BS>(p, c, (int)blockIdx.x / p.num_kv_heads, (int)blockIdx.x % p.num_kv_heads, s_buf0,
+                               s_buf1, s_buf2, s_blk, s_live);
+  } else {
+    const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+    const int tail_wgs = (int)gridDim.x - prefix_wgs;
+    tail_role<QT, CT, D, BS>(p, c, ((int)blockIdx.x - prefix_wgs) * kCascadeWaves + wave, tail_wgs * kCascadeWaves);
+  }
+}
+
+// One wavefront per (sequence, KV head) item with a prefix: the tail state
+// and the prefix chunks' states folded into one softmax, the row written.
+template <class QT, int D, int BS>
+__global__ __launch_bounds__(64 * kMergeItemsPerWorkgroup) void paged_cascade_merge_kernel(DecodeParams p,
+                                                                                          CascadeParams c) {
+  using QS = typename Elem<QT>::storage;
+  constexpr int DT = Tile<D>::DT;
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4, col = lane & 15;
+  const int item = (int)blockIdx.x * kMergeItemsPerWorkgroup + (int)(threadIdx.x >> 6);
+  if (item >= p.num_seqs * p.units) return;
+  const int seq = item / p.units;
+  int kvh, h0, nh;
+  unit_heads(p, item - seq * p.units, kvh, h0, nh);
+  const uint32_t ctx = (uint32_t)p.context_lens[seq];
+  const bool live = ctx != 0 && ctx <= (uint32_t)p.max_seq_len;
+  const int pre = usable_prefix<BS>(c, seq, live);
+  if (pre == 0) return;  // written by the tail role
+  WaveAcc<D> acc;
+  acc.init();
+  if (col < nh) {
+    const int64_t row = (int64_t)seq * p.num_heads + h0 + col;
+    const float2 ml = *reinterpret_cast<const float2*>(c.ws_tail_ml + row * 2);
+    float4 o[DT];
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) o[dt] = *reinterpret_cast<const float4*>(c.ws_tail_o + row * D + 16 * dt + 4 * g);
+    fold_partial<D>(acc, ml.x, ml.y, o, g);
+  }
+  fold_prefix<D>(c, ((int64_t)seq * p.num_heads + h0) * c.max_chunks, nh, (pre + c.chunk - 1) / c.chunk, g, col, acc);
+  const float L = column_sum(acc.l_run);
+  if (col >= nh) return;
+  const float inv = p.v_scale / (L + 1e-6f);
+  QS* out = static_cast<QS*>(p.out) + ((int64_t)seq * p.num_heads + h0 + col) * D;
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+    store4<QT>(out + 16 * dt + 4 * g, acc.o[dt][0] * inv, acc.o[dt][1] * inv, acc.o[dt][2] * inv, acc.o[dt][3] * inv);
+}
+
+template <class QT, class CT, int D, int BS>
+static hipError_t launch_cascade_bs(const DecodeParams& p, const CascadeParams& c, hipStream_t stream) {
+  const int64_t items = (int64_t)p.num_seqs * p.units;
+  const int64_t prefix_wgs = (int64_t)c.num_tiles * p.num_kv_heads;
+  // One tail wavefront per item; the hardware deals the tail workgroups to
+  // CUs as slots free up, longest tails first.
+  const int64_t tail_wgs = (items + kCascadeWaves - 1) / kCascadeWaves;
+  hipLaunchKernelGGL((paged_cascade_kernel<QT, CT, D, BS>), dim3((unsigned)(prefix_wgs + tail_wgs)),
+                     dim3(64 * kCascadeWaves), 0, stream, p, c);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || c.num_tiles == 0) return e;
+  hipLaunchKernelGGL((paged_cascade_merge_kernel<QT, D, BS>),
+                     dim3((unsigned)((items + kMergeItemsPerWorkgroup - 1) / kMergeItemsPerWorkgroup)),
+                     dim3(64 * kMergeItemsPerWorkgroup), 0, stream, p, c);
+  return hipGetLastError();
+}
+
+template <class QT, class CT, int D>
+static hipError_t launch_cascade_d(const DecodeParams& p, const CascadeParams& c, int block_size, hipStream_t stream,
+                                   bool* ok) {
+  switch (block_size) {
+    case 8:
+      // FP8 V tiles of 8-token blocks are 8 bytes per dimension, below the
+      // 16-byte direct-to-LDS unit: the one-pass decode takes them.
+      if constexpr (std::is_same<CT, FP8>::value) break;
+      else return launch_cascade_bs<QT, CT, D, 8>(p, c, stream);
+    case 16: return launch_cascade_bs<QT, CT, D, 16>(p, c, stream);
+    case 32: return launch_cascade_bs<QT, CT, D, 32>(p, c, stream);
+  }
+  *ok = false;
+  return hipErrorInvalidValue;
+}
+
+template <class QT, class CT>
+hipError_t launch_cascade_typed(const DecodeParams& p, const CascadeParams& c, int head_size, int block_size,
+                                hipStream_t stream, bool* ok) {
+  // Query sets of 16 columns: the GQA group of a KV head fits one set.
+  if (p.slices != 1 || p.rows) {
+    *ok = false;
+    return hipErrorInvalidValue;
+  }
+  switch (head_size) {
+    case 64: return launch_cascade_d<QT, CT, 64>(p, c, block_size, stream, ok);
+    case 128: return launch_cascade_d<QT, CT, 128>(p, c, block_size, stream, ok);
+  }
+  *ok = false;
+  return hipErrorInvalidValue;
+}
+
+}  // namespace pkv

@@ -128,6 +128,17 @@ DecodeWorkspace decode_workspace_layout(int32_t num_seqs, int32_t num_heads, int
   w.total = w.ml_bytes + w.o_bytes;
   return w;
 }
+CascadeWorkspace cascade_workspace_layout(int32_t num_seqs, int32_t num_heads, int32_t head_size,
+                                          int32_t max_chunks) {
+  CascadeWorkspace w;
+  auto align = [](size_t x) { return (x + 255) & ~size_t(255); };
+  w.ml_bytes = align((size_t)num_seqs * num_heads * max_chunks * 2 * sizeof(float));
+  w.o_bytes = align((size_t)num_seqs * num_heads * max_chunks * head_size * sizeof(float));
+  w.tail_ml_bytes = align((size_t)num_seqs * num_heads * 2 * sizeof(float));
+  w.tail_o_bytes = align((size_t)num_seqs * num_heads * head_size * sizeof(float));
+  w.total = w.ml_bytes + w.o_bytes + w.tail_ml_bytes + w.tail_o_bytes;
+  return w;
+}
 }  // namespace pkv
 
 extern "C" {
@@ -212,6 +223,13 @@ size_t pkv_paged_attention_workspace_size(int32_t num_seqs, int32_t num_heads, i
   return pkv::decode_workspace_layout(num_seqs, num_heads, head_size, parts).total;
 }
 
+size_t pkv_paged_attention_cascade_workspace_size(int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
+                                                  int32_t head_size, int32_t max_seq_len, int32_t max_chunks) {
+  const size_t v1 = pkv_paged_attention_workspace_size(num_seqs, num_heads, num_kv_heads, head_size, max_seq_len, 0);
+  if (v1 == 0 || max_chunks <= 0 || max_chunks > 65536) return 0;
+  return std::max(v1, pkv::cascade_workspace_layout(num_seqs, num_heads, head_size, max_chunks).total);
+}
+
 }  // extern "C"
 
 namespace {
@@ -254,7 +272,8 @@ int paged_attention_impl(void* out, const void* query, const void* key_cache, co
                          int64_t num_blocks, float scale, int64_t q_stride, int64_t k_block_stride,
                          int64_t k_head_stride, int64_t v_block_stride, int64_t v_head_stride, int32_t layout,
                          int32_t partition_size, void* workspace, size_t workspace_bytes, bool use_scratch,
-                         int32_t q_dtype, int32_t cache_dtype, float k_scale, float v_scale, void* stream) {
+                         int32_t q_dtype, int32_t cache_dtype, float k_scale, float v_scale, void* stream,
+                         const pkv_cascade_plan* plan = nullptr) {
   if (num_seqs < 0) return fail(PKV_ERR_INVALID, "num_seqs must be non-negative");
   int32_t ps = 0, parts = 0;
   const int st = resolve_partition(num_seqs, num_heads, num_kv_heads, max_seq_len, block_size, partition_size,
@@ -307,7 +326,39 @@ int paged_attention_impl(void* out, const void* query, const void* key_cache, co
       (reinterpret_cast<uintptr_t>(value_cache) % v_align) != 0 || (vbs * cb) % v_align != 0 ||
       (v_head_stride * cb) % v_align != 0)
     return fail(PKV_ERR_INVALID, "cache base or strides are not aligned for vector loads");
+  if (plan != nullptr) {
+    if (plan->prefix_lens == nullptr || plan->order == nullptr)
+      return fail(PKV_ERR_INVALID, "cascade plan: prefix_lens and order are required");
+    if (plan->num_tiles < 0 || plan->num_members < 0)
+      return fail(PKV_ERR_INVALID, "cascade plan: num_tiles and num_members must be non-negative");
+    if (plan->num_tiles > 0 && (plan->members == nullptr || plan->tiles == nullptr || plan->num_members == 0))
+      return fail(PKV_ERR_INVALID, "cascade plan: tiles need members");
+    if (plan->tiles != nullptr && !aligned16(plan->tiles))
+      return fail(PKV_ERR_INVALID, "cascade plan: tiles must be 16-byte aligned");
+    if (plan->chunk_tokens <= 0 || plan->chunk_tokens % pkv::kTile != 0 || plan->chunk_tokens % block_size != 0 ||
+        plan->chunk_tokens > pkv::kMaxPrefixChunk)
+      return fail(PKV_ERR_INVALID, "cascade plan: chunk_tokens must be a positive multiple of 16 and of block_size, "
+                                   "at most 4096");
+    if (plan->max_chunks <= 0 || plan->max_chunks > 65536 || plan->max_tail < 0)
+      return fail(PKV_ERR_INVALID, "cascade plan: max_chunks must be in [1, 65536] and max_tail non-negative");
+    if ((int64_t)num_seqs * num_heads * plan->max_chunks * head_size > ((int64_t)1 << 40))
+      return fail(PKV_ERR_UNSUPPORTED, "cascade plan: workspace beyond 4 TiB");
+  }
+  // The cascade kernels: 16-bit queries over caches of the same type or
+  // FP8, head sizes 64 and 128, GQA groups of at most 16, tails of at most
+  // kTailMaxTokens, and V rows aligned for 16-byte loads.  Other shapes take
+  // the one-pass decode below, whose result is the same.
+  const bool cascade = plan != nullptr && !rows && (q_dtype == PKV_BF16 || q_dtype == PKV_F16) &&
+                       (cache_dtype == q_dtype || (fp8 && block_size >= 16)) &&
+                       (head_size == 64 || head_size == 128) &&
+                       num_heads / num_kv_heads <= 16 && plan->max_tail <= pkv::kTailMaxTokens &&
+                       aligned16(value_cache) && (vbs * cb) % 16 == 0 && (v_head_stride * cb) % 16 == 0;
   const pkv::DecodeWorkspace w = pkv::decode_workspace_layout(num_seqs, num_heads, head_size, parts);
+  const pkv::CascadeWorkspace cw =
+      plan != nullptr ? pkv::cascade_workspace_layout(num_seqs, num_heads, head_size, plan->max_chunks)
+                      : pkv::CascadeWorkspace{0, 0, 0, 0, 0};
+  if (cascade && (workspace == nullptr || workspace_bytes < cw.total))
+    return fail(PKV_ERR_INVALID, "workspace is smaller than pkv_paged_attention_cascade_workspace_size()");
   if (use_scratch) {
     if (w.total > (size_t)PKV_NOALLOC_SCRATCH_BYTES)
       return fail(PKV_ERR_UNSUPPORTED, "pkv_paged_attention_noalloc needs " + std::to_string(w.total) +
@@ -371,6 +422,33 @@ int paged_attention_impl(void* out, const void* query, const void* key_cache, co
   hipError_t e = hipErrorInvalidValue;
   const hipStream_t s = static_cast<hipStream_t>(stream);
   clear_pending_error();
+  if (cascade) {
+    pkv::CascadeParams c;
+    c.prefix_lens = plan->prefix_lens;
+    c.order = plan->order;
+    c.members = plan->members;
+    c.tiles = reinterpret_cast<const int4*>(plan->tiles);
+    c.ws_ml = reinterpret_cast<float*>(ws);
+    c.ws_o = reinterpret_cast<float*>(ws + cw.ml_bytes);
+    c.ws_tail_ml = reinterpret_cast<float*>(ws + cw.ml_bytes + cw.o_bytes);
+    c.ws_tail_o = reinterpret_cast<float*>(ws + cw.ml_bytes + cw.o_bytes + cw.tail_ml_bytes);
+    c.num_members = plan->num_members;
+    c.num_tiles = plan->num_tiles;
+    c.chunk = plan->chunk_tokens;
+    c.max_chunks = plan->max_chunks;
+    c.max_tail = plan->max_tail;
+    if (q_dtype == PKV_BF16)
+      e = fp8 ? pkv::launch_cascade_typed<pkv::BF16, pkv::FP8>(p, c, head_size, block_size, s, &ok)
+              : pkv::launch_cascade_typed<pkv::BF16, pkv::BF16>(p, c, head_size, block_size, s, &ok);
+    else
+      e = fp8 ? pkv::launch_cascade_typed<pkv::F16, pkv::FP8>(p, c, head_size, block_size, s, &ok)
+              : pkv::launch_cascade_typed<pkv::F16, pkv::F16>(p, c, head_size, block_size, s, &ok);
+    if (ok) {
+      if (e != hipSuccess) return hip_fail(e, "paged_attention_cascade launch");
+      return PKV_OK;
+    }
+    ok = true;  // a shape the cascade kernels do not take: the one-pass decode
+  }
   if (fp8) {
     if (q_dtype == PKV_BF16)
       e = pkv::launch_decode_typed<pkv::BF16, pkv::FP8>(p, head_size, block_size, s, &ok);
@@ -426,6 +504,23 @@ int pkv_paged_attention_noalloc(void* out, const void* query, const void* key_ca
                               num_blocks, scale, q_stride, k_block_stride, k_head_stride, v_block_stride,
                               v_head_stride, layout, partition_size, nullptr, 0, true, q_dtype, cache_dtype,
                               k_scale, v_scale, stream);
+}
+
+int pkv_paged_attention_cascade(void* out, const void* query, const void* key_cache, const void* value_cache,
+                                const int32_t* block_tables, const int32_t* context_lens, const float* alibi_slopes,
+                                const pkv_cascade_plan* plan, int32_t num_seqs, int32_t num_heads,
+                                int32_t num_kv_heads, int32_t head_size, int32_t block_size,
+                                int32_t max_num_blocks_per_seq, int32_t max_seq_len, int64_t num_blocks, float scale,
+                                int64_t q_stride, int64_t k_block_stride, int64_t k_head_stride,
+                                int64_t v_block_stride, int64_t v_head_stride, void* workspace,
+                                size_t workspace_bytes, int32_t q_dtype, int32_t cache_dtype, float k_scale,
+                                float v_scale, void* stream) {
+  if (plan == nullptr) return fail(PKV_ERR_INVALID, "cascade plan is null");
+  return paged_attention_impl(out, query, key_cache, value_cache, block_tables, context_lens, alibi_slopes, num_seqs,
+                              num_heads, num_kv_heads, head_size, block_size, max_num_blocks_per_seq, max_seq_len,
+                              num_blocks, scale, q_stride, k_block_stride, k_head_stride, v_block_stride,
+                              v_head_stride, PKV_LAYOUT_PAGED5D, 0, workspace, workspace_bytes, false, q_dtype,
+                              cache_dtype, k_scale, v_scale, stream, plan);
 }
 
 int pkv_max_shared_memory_per_block(int32_t device_id, int64_t* out) {

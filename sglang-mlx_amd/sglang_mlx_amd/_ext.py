@@ -21,6 +21,7 @@ Deliberate differences from the reference, all on inputs it cannot serve:
 
 from __future__ import annotations
 
+import ctypes
 import math
 import threading
 
@@ -186,8 +187,31 @@ def _check_paged_attention(query, key_cache, value_cache, block_tables, context_
     return qc, cc, layout
 
 
+def _plan_struct(plan, B: int, dev: torch.device):
+    """The ctypes pkv_cascade_plan of a CascadePlan (checked: int32 tensors
+    on the query's device, contiguous, with the shapes the header states)."""
+    arrays = {}
+    for name, shape in (("prefix_lens", (B,)), ("order", (B,)), ("members", None), ("tiles", None)):
+        t = getattr(plan, name)
+        if not isinstance(t, torch.Tensor) or t.dtype != torch.int32 or t.device != dev or not t.is_contiguous():
+            raise ValueError(f"cascade plan: {name} must be a contiguous int32 tensor on {dev}")
+        if shape is not None and tuple(t.shape) != shape:
+            raise ValueError(f"cascade plan: {name} must have shape {list(shape)}")
+        arrays[name] = t
+    tiles = arrays["tiles"]
+    if tiles.dim() != 2 or tiles.shape[1] != 4:
+        raise ValueError("cascade plan: tiles must have shape [num_tiles, 4]")
+    if arrays["members"].dim() != 1:
+        raise ValueError("cascade plan: members must be 1-D")
+    ptr = lambda t: t.data_ptr() if t.numel() else None  # noqa: E731
+    return _lib.CascadePlanC(ptr(arrays["prefix_lens"]), ptr(arrays["order"]), ptr(arrays["members"]), ptr(tiles),
+                             arrays["members"].numel(), tiles.shape[0], int(plan.chunk_tokens),
+                             int(plan.max_chunks), int(plan.max_tail))
+
+
 def _paged_attention(op, query, key_cache, value_cache, block_tables, context_lens, num_kv_heads,
-                     scale, block_size, max_seq_len, alibi_slopes, partition_size, k_scale=1.0, v_scale=1.0):
+                     scale, block_size, max_seq_len, alibi_slopes, partition_size, k_scale=1.0, v_scale=1.0,
+                     plan=None):
     for t in (query, key_cache, value_cache, block_tables, context_lens):
         _tensor(t)
     _tensor(alibi_slopes, allow_none=True)
@@ -210,6 +234,26 @@ def _paged_attention(op, query, key_cache, value_cache, block_tables, context_le
     if B == 0:
         return out
     lib = _lib.lib()
+    if plan is not None:
+        if layout != _lib.PKV_LAYOUT_PAGED5D:
+            raise ValueError("paged_attention_cascade reads the paged 5-D layout")
+        cplan = _plan_struct(plan, B, dev)
+        with torch.cuda.device(dev):
+            stream = _stream(dev)
+            need = lib.pkv_paged_attention_cascade_workspace_size(B, Hq, num_kv_heads, D, max_seq_len,
+                                                                  int(plan.max_chunks))
+            if need == 0:
+                raise ValueError("cascade plan: invalid sizes (max_chunks must be in [1, 65536])")
+            ws = _decode_scratch(dev, stream, need)
+            st = lib.pkv_paged_attention_cascade(
+                out.data_ptr(), query.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
+                bt.data_ptr(), lens.data_ptr(), None if alibi is None else alibi.data_ptr(), ctypes.byref(cplan),
+                B, Hq, num_kv_heads, D, block_size, bt.shape[1], max_seq_len, key_cache.shape[0],
+                float(scale), query.stride(0), key_cache.stride(0), key_cache.stride(1),
+                value_cache.stride(0), value_cache.stride(1), ws.data_ptr(), ws.numel(), qc, cc, k_scale, v_scale,
+                stream)
+        _lib.check(st)
+        return out
     with torch.cuda.device(dev):
         stream = _stream(dev)
         need = lib.pkv_paged_attention_workspace_size(B, Hq, num_kv_heads, D, max_seq_len,
@@ -255,6 +299,21 @@ def paged_attention_v2(query, key_cache, value_cache, block_tables, seq_lens, nu
     return _paged_attention("PagedAttentionV2", query, key_cache, value_cache, block_tables, seq_lens,
                             num_kv_heads, scale, block_size, max_seq_len, alibi_slopes, partition_size,
                             k_scale, v_scale)
+
+
+def paged_attention_cascade(query, key_cache, value_cache, block_tables, seq_lens, num_kv_heads,
+                            scale, block_size, max_seq_len, plan, alibi_slopes=None, k_scale=1.0,
+                            v_scale=1.0):
+    """paged_attention_v1 with radix-shared prefixes computed once per
+    group: ``plan`` (srt.mem_cache.build_cascade_plan) lists the sequences
+    whose block tables begin with the same blocks.  A prefix pass attends
+    every member's query rows to the shared tokens at once; a tail pass
+    streams each sequence's remaining tokens and folds the prefix state in.
+    Same arguments and result as ``paged_attention_v1`` (paged 5-D caches);
+    shapes the cascade kernels do not cover run the one-pass decode."""
+    return _paged_attention("PagedAttentionCascade", query, key_cache, value_cache, block_tables, seq_lens,
+                            num_kv_heads, scale, block_size, max_seq_len, alibi_slopes, 0, k_scale, v_scale,
+                            plan=plan)
 
 
 def _reshape_and_cache(op, key, value, key_cache, value_cache, slot_mapping, flash: bool,

@@ -29,6 +29,25 @@ _i64 = ctypes.c_int64
 _size = ctypes.c_size_t
 _f32 = ctypes.c_float
 
+
+
+class CascadePlanC(ctypes.Structure):
+    """pkv_cascade_plan (include/pagedkv.h): device pointers and sizes of a
+    shared-prefix plan."""
+
+    _fields_ = [
+        ("prefix_lens", _c_void_p),
+        ("order", _c_void_p),
+        ("members", _c_void_p),
+        ("tiles", _c_void_p),
+        ("num_members", _i32),
+        ("num_tiles", _i32),
+        ("chunk_tokens", _i32),
+        ("max_chunks", _i32),
+        ("max_tail", _i32),
+    ]
+
+
 # name -> (restype, argtypes); the tests check this table against the header.
 SIGNATURES = {
     "pkv_version": (ctypes.c_char_p, []),
@@ -51,6 +70,19 @@ SIGNATURES = {
         _f32, _i64,                                               # scale, q_stride
         _i64, _i64, _i64, _i64,                                   # k/v block & head strides
         _i32, _i32,                                               # layout, partition_size
+        _c_void_p, _size,                                         # workspace, bytes
+        _i32, _i32,                                               # q dtype, cache dtype
+        _f32, _f32, _c_void_p,                                    # k_scale, v_scale (FP8), stream
+    ]),
+    "pkv_paged_attention_cascade_workspace_size": (_size, [_i32, _i32, _i32, _i32, _i32, _i32]),
+    "pkv_paged_attention_cascade": (ctypes.c_int, [
+        _c_void_p, _c_void_p, _c_void_p, _c_void_p,              # out, q, kc, vc
+        _c_void_p, _c_void_p, _c_void_p,                          # block_tables, ctx, alibi
+        ctypes.POINTER(CascadePlanC),                             # plan
+        _i32, _i32, _i32, _i32, _i32,                             # B, Hq, Hkv, D, bs
+        _i32, _i32, _i64,                                         # max_blocks, max_seq_len, nb
+        _f32, _i64,                                               # scale, q_stride
+        _i64, _i64, _i64, _i64,                                   # k/v block & head strides
         _c_void_p, _size,                                         # workspace, bytes
         _i32, _i32,                                               # q dtype, cache dtype
         _f32, _f32, _c_void_p,                                    # k_scale, v_scale (FP8), stream

@@ -5,6 +5,8 @@ tensors.
 Operations:
     paged_attention_v1   single-softmax paged decode attention
     paged_attention_v2   split-K paged decode with a log-sum-exp merge
+    paged_attention_cascade  decode with radix-shared prefixes computed once
+                         per group of sequences (a host-built plan)
     reshape_and_cache    scatter new KV tokens into the cache (in place)
     copy_blocks          block copies inside the caches
     swap_blocks          block copies between two buffers
@@ -80,6 +82,29 @@ def paged_attention_v2(
     return _ext.paged_attention_v2(query, key_cache, value_cache, block_tables, context_lens,
                                    num_kv_heads, scale, block_size, max_seq_len, alibi_slopes,
                                    partition_size, k_scale, v_scale)
+
+
+def paged_attention_cascade(
+    query: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    context_lens: torch.Tensor,
+    num_kv_heads: int,
+    scale: float,
+    block_size: int,
+    max_seq_len: int,
+    plan,
+    alibi_slopes: torch.Tensor | None = None,
+    k_scale: float = 1.0,
+    v_scale: float = 1.0,
+) -> torch.Tensor:
+    """Paged attention with radix-shared prefixes computed once per group of
+    sequences (``plan``: srt.mem_cache.build_cascade_plan over the same block
+    tables).  Same arguments and result as ``paged_attention_v1`` (paged 5-D
+    caches), to within floating-point rounding."""
+    return _ext.paged_attention_cascade(query, key_cache, value_cache, block_tables, context_lens, num_kv_heads,
+                                        scale, block_size, max_seq_len, plan, alibi_slopes, k_scale, v_scale)
 
 
 def reshape_and_cache(

@@ -8,11 +8,13 @@ from .cache_init_params import CacheInitParams
 from .evict_policy import (EvictionStrategy, FIFOStrategy, FILOStrategy, LFUStrategy, LRUStrategy, MRUStrategy,
                            PriorityStrategy)
 from .memory_pool import MHATokenPool, PooledKVCache, TokenPoolAllocator, decode_batch
-from .paged_pool import BlockAllocator, BlockRadixCache, BlockTable, build_block_tables
+from .paged_pool import (BlockAllocator, BlockRadixCache, BlockTable, CascadePlan, build_block_tables,
+                         build_cascade_plan, plan_prefix_groups)
 from .radix_cache import RadixCache, TreeNode
 
 __all__ = [
-    "BasePrefixCache", "BlockAllocator", "BlockRadixCache", "BlockTable", "build_block_tables", "CacheInitParams", "EvictParams", "EvictResult", "EvictionStrategy", "FIFOStrategy",
+    "BasePrefixCache", "BlockAllocator", "BlockRadixCache", "BlockTable", "build_block_tables", "build_cascade_plan",
+    "CascadePlan", "plan_prefix_groups", "CacheInitParams", "EvictParams", "EvictResult", "EvictionStrategy", "FIFOStrategy",
     "FILOStrategy", "InsertParams", "InsertResult", "LFUStrategy", "LRUStrategy", "MHATokenPool", "MRUStrategy",
     "MatchResult", "PooledKVCache", "PriorityStrategy", "decode_batch", "RadixCache", "TokenPoolAllocator", "TreeNode",
 ]

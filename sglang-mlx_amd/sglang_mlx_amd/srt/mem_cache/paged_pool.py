@@ -28,6 +28,7 @@ tables, so this module keeps the same structures at block granularity:
 from __future__ import annotations
 
 import time
+from dataclasses import dataclass, field
 from typing import Callable, Iterable
 
 import numpy as np
@@ -172,6 +173,124 @@ def build_block_tables(tables: list[BlockTable], max_blocks: int | None = None) 
         out[i, :len(t.blocks)] = t.blocks
         ctx[i] = t.num_tokens
     return out, ctx
+
+
+PREFIX_ROWS = 128          # query rows of one prefix-pass workgroup
+PREFIX_MAX_CHUNK = 4096    # longest prefix chunk of one prefix-pass workgroup
+PREFIX_MIN_CHUNK = 256
+
+
+@dataclass
+class CascadePlan:
+    """Shared-prefix plan of paged_attention_cascade (the pkv_cascade_plan of
+    include/pagedkv.h).  Device tensors are int32; ``groups`` keeps the
+    host-side (members, prefix tokens) of each group for inspection."""
+
+    prefix_lens: "torch.Tensor"
+    order: "torch.Tensor"
+    members: "torch.Tensor"
+    tiles: "torch.Tensor"
+    chunk_tokens: int
+    max_chunks: int
+    max_tail: int
+    groups: list = field(default_factory=list)
+
+
+def plan_prefix_groups(block_tables: np.ndarray, context_lens: np.ndarray, block_size: int,
+                       min_members: int = 2, min_shared_tokens: int = 0) -> list[tuple[np.ndarray, int]]:
+    """Groups of sequences whose block tables begin with the same blocks:
+    [(member sequence ids, shared prefix tokens)].  Sequences are grouped by
+    their first block id; a group's prefix is the longest run of leading
+    blocks that every member maps to the same ids and holds in full (so it
+    ends at or before each member's context).  Groups with fewer than
+    ``min_members`` members, or whose sharing saves fewer than
+    ``min_shared_tokens`` token reads ((members - 1) * prefix), are dropped."""
+    bt = np.asarray(block_tables)
+    ctx = np.asarray(context_lens).astype(np.int64)
+    B = bt.shape[0]
+    full = np.minimum(ctx // block_size, bt.shape[1]) if B else ctx
+    cand = np.nonzero((full >= 1) & (bt[:, 0] >= 0))[0] if B else np.zeros(0, dtype=np.int64)
+    groups = []
+    if cand.size == 0:
+        return groups
+    first = bt[cand, 0]
+    order = np.argsort(first, kind="stable")
+    cand, first = cand[order], first[order]
+    cuts = np.nonzero(np.diff(first))[0] + 1
+    for mem in np.split(cand, cuts):
+        if mem.size < max(min_members, 2):
+            continue
+        kmax = int(full[mem].min())
+        rows = bt[mem, :kmax]
+        same = (rows == rows[0]).all(axis=0)
+        k = kmax if same.all() else int(np.argmin(same))
+        prefix = k * block_size
+        if k == 0 or (mem.size - 1) * prefix < min_shared_tokens:
+            continue
+        groups.append((np.sort(mem).astype(np.int32), prefix))
+    return groups
+
+
+def build_cascade_plan(block_tables: np.ndarray, context_lens: np.ndarray, block_size: int, num_heads: int,
+                       num_kv_heads: int, device=None, num_cus: int = 256, min_members: int = 2,
+                       min_shared_tokens: int = 0, chunk_tokens: int | None = None) -> CascadePlan:
+    """The paged_attention_cascade plan of a batch from its host-side int32
+    block tables [B, max_blocks] and context lengths [B]
+    (build_block_tables' output).  Work units of the prefix pass are
+    (up to 128 // group members of a group) x (one chunk of its prefix);
+    the chunk is the longest power of two in [256, 4096] tokens (a multiple
+    of block_size and 16) that still gives every one of ``num_cus`` CUs a
+    workgroup (units x KV heads), unless ``chunk_tokens`` fixes it."""
+    import torch
+
+    bt = np.asarray(block_tables, dtype=np.int32)
+    ctx = np.asarray(context_lens).astype(np.int64)
+    B = bt.shape[0]
+    if num_kv_heads <= 0 or num_heads % num_kv_heads:
+        raise ValueError("num_heads must be divisible by num_kv_heads")
+    group = num_heads // num_kv_heads
+    per_tile = max(1, PREFIX_ROWS // group)
+    groups = plan_prefix_groups(bt, ctx, block_size, min_members, min_shared_tokens)
+    step = int(np.lcm(16, block_size))
+    if chunk_tokens is None:
+        chunk = PREFIX_MAX_CHUNK
+        row_tiles = sum(-(-m.size // per_tile) for m, _ in groups)
+
+        def units(ch):
+            return sum(-(-m.size // per_tile) * -(-p // ch) for m, p in groups) * num_kv_heads
+
+        while chunk > PREFIX_MIN_CHUNK and row_tiles and units(chunk) < num_cus:
+            chunk //= 2
+        chunk = max(step, chunk - chunk % step)
+    else:
+        chunk = int(chunk_tokens)
+        if chunk <= 0 or chunk % step or chunk > PREFIX_MAX_CHUNK:
+            raise ValueError("chunk_tokens must be a positive multiple of 16 and of block_size, at most 4096")
+    prefix_lens = np.zeros(B, dtype=np.int32)
+    members, tiles = [], []
+    max_chunks = 1
+    for mem, p in groups:
+        base = len(members)
+        members.extend(mem.tolist())
+        prefix_lens[mem] = p
+        nch = -(-p // chunk)
+        max_chunks = max(max_chunks, nch)
+        for m0 in range(0, mem.size, per_tile):
+            mc = min(per_tile, mem.size - m0)
+            for c in range(nch):
+                tiles.append((base + m0, mc, c * chunk, min(p, (c + 1) * chunk)))
+    tail = np.maximum(ctx - prefix_lens, 0)
+    order = np.argsort(-tail, kind="stable").astype(np.int32)
+    dev = torch.device(device) if device is not None else torch.device("cpu")
+
+    def t(a, shape=None):
+        x = torch.as_tensor(np.asarray(a, dtype=np.int32).reshape(shape) if shape else np.asarray(a, dtype=np.int32))
+        return x.to(dev)
+
+    return CascadePlan(prefix_lens=t(prefix_lens), order=t(order), members=t(members),
+                       tiles=t(tiles if tiles else np.zeros((0, 4), dtype=np.int32), (-1, 4)),
+                       chunk_tokens=chunk, max_chunks=max_chunks, max_tail=int(tail.max()) if B else 0,
+                       groups=groups)
 
 
 class BlockRadixCache:

@@ -14,7 +14,7 @@ ones, but in the shuffled order: blocks move between sequences and positions
 (freeing and re-allocating in one order would give every position its own
 block back).  Each re-allocated block's tokens are rewritten through
 reshape_and_cache into every layer pool, and the int32 tables and context
-lengths are rebuilt.
+lengths are rebuilt, and so is the shared-prefix plan of paged_attention_cascade.
 """
 
 from __future__ import annotations
@@ -100,9 +100,22 @@ class RadixSharedWorkload:
         bt, ctx = self.block_tables()
         return dict(victims=victims, freed=freed, fresh=fresh, slots=slots, bt=bt, ctx=ctx,
                     bt_dev=torch.from_numpy(bt).to(self.dev, non_blocking=True),
-                    ctx_dev=torch.from_numpy(ctx).to(self.dev, non_blocking=True))
+                    ctx_dev=torch.from_numpy(ctx).to(self.dev, non_blocking=True),
+                    plan=self.plan(bt, ctx))
+
+    def plan(self, bt, ctx):
+        """The shared-prefix plan of the current tables (host work, like the
+        tables themselves)."""
+        from sglang_mlx_amd.srt.mem_cache import build_cascade_plan
+
+        return build_cascade_plan(bt, ctx, BS, HQ, HKV, device=self.dev)
 
     def decode(self, layer: int, bt_dev, ctx_dev):
         kc, vc = self.pools[layer]
         return self.kernels.paged_attention_v1(self.q, kc, vc, bt_dev, ctx_dev, HKV, self.scale, BS,
                                                self.max_seq_len, **self.scales)
+
+    def decode_cascade(self, layer: int, bt_dev, ctx_dev, plan):
+        kc, vc = self.pools[layer]
+        return self.kernels.paged_attention_cascade(self.q, kc, vc, bt_dev, ctx_dev, HKV, self.scale, BS,
+                                                    self.max_seq_len, plan, **self.scales)

@@ -12,7 +12,9 @@ block in two rows or in the prefix, one slot per logical token).
 GPU: the same steps on real caches (bf16 and FP8 E4M3).  After each step the
 whole layer pool equals the oracle's append applied to a host copy, bit for
 bit, and the decode of all 256 sequences x 32 heads matches the oracle on
-the current tables (bf16 query: 1e-2 abs / 2e-2 rel)."""
+the current tables (bf16 query: 1e-2 abs / 2e-2 rel), through
+paged_attention_v1 and through paged_attention_cascade with the plan rebuilt
+from the churned tables."""
 
 import numpy as np
 import pytest
@@ -140,3 +142,9 @@ def test_full_shape_with_churn_on_gpu(cache):
         ref = orc.paged_attention(q_np, kc_np, vc_np, info["bt"], info["ctx"], 8, w.scale, BS, w.max_seq_len,
                                   None, "bfloat16", cache, ks, vs)
         np.testing.assert_allclose(to_f64(out), ref, atol=1e-2, rtol=2e-2, err_msg=f"churn step {step}")
+        # The shared-prefix (cascade) decode of the same step, with the plan
+        # rebuilt from the churned tables.
+        assert info["plan"].groups[0][1] == SHARED_BLOCKS * BS
+        outc = w.decode_cascade(0, info["bt_dev"], info["ctx_dev"], info["plan"])
+        torch.cuda.synchronize()
+        np.testing.assert_allclose(to_f64(outc), ref, atol=1e-2, rtol=2e-2, err_msg=f"cascade, churn step {step}")
