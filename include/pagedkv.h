@@ -198,14 +198,12 @@ int pkv_paged_attention(void* out, const void* query, const void* key_cache,
 
 /*
  * Shared-prefix plan of pkv_paged_attention_cascade, built on the host from
- * the block tables (sglang_mlx_amd.srt.mem_cache.build_cascade_plan).  All
- * arrays are int32 device buffers.
+ * the block tables and context lengths
+ * (sglang_mlx_amd.srt.mem_cache.build_cascade_plan).  All arrays are int32
+ * device buffers.
  *   prefix_lens [num_seqs]: leading tokens of each sequence that the prefix
  *                pass covers, 0 for none; a multiple of block_size and of 16
  *                (of 8 for 8-token blocks), at most the sequence's context.
- *   order       [num_seqs]: the sequences by descending tail length
- *                (context - prefix), a permutation of 0 .. num_seqs-1; it
- *                only schedules the tail pass.
  *   members     [num_members]: sequence ids, each prefix group's members
  *                adjacent.
  *   tiles       [num_tiles][4] (16-byte aligned): (member_begin,
@@ -218,28 +216,38 @@ int pkv_paged_attention(void* out, const void* query, const void* key_cache,
  *                The units of a group cover its prefix [0, prefix_len)
  *                chunk by chunk, and every member sits in the units of its
  *                group.
+ *   parts       [num_parts][2] (8-byte aligned): (sequence, k) of each tail
+ *                partition, the order the tail pass takes them in (longest
+ *                first balances the launch).  Partition k of a sequence
+ *                covers tokens [pre + k * part_tokens, min(context, pre +
+ *                (k + 1) * part_tokens)) after its prefix pre; every
+ *                sequence, whatever its context, has max(1, ceil((context
+ *                - pre) / part_tokens)) partitions, each listed once.
  *   chunk_tokens: a multiple of 16 and of block_size, at most 4096.
  *   max_chunks  : at least ceil(prefix_lens[s] / chunk_tokens) for every s.
- *   max_tail    : the longest context - prefix_lens[s] over the sequences.
+ *   part_tokens : a multiple of 16 and of block_size, at most 1024.
+ *   max_parts   : at least the partitions of every sequence.
  * A plan that breaks these rules never makes a kernel read or write outside
  * its buffers, but the rows it concerns are then undefined.
  */
 typedef struct pkv_cascade_plan {
   const int32_t* prefix_lens;
-  const int32_t* order;
   const int32_t* members;
   const int32_t* tiles;
+  const int32_t* parts;
   int32_t num_members;
   int32_t num_tiles;
+  int32_t num_parts;
   int32_t chunk_tokens;
   int32_t max_chunks;
-  int32_t max_tail;
+  int32_t part_tokens;
+  int32_t max_parts;
 } pkv_cascade_plan;
 
 /*
  * Workspace bytes of pkv_paged_attention_cascade: the larger of the one-pass
  * decode's (pkv_paged_attention_workspace_size with partition_size 0) and
- * the partial states' (num_seqs * num_heads * (max_chunks + 1) *
+ * the partial states' (num_seqs * num_heads * (max_chunks + max_parts) *
  * (head_size + 2) float32, in four parts each 256-byte aligned).  Returns 0
  * for invalid sizes.
  */
@@ -248,7 +256,8 @@ size_t pkv_paged_attention_cascade_workspace_size(int32_t num_seqs,
                                                   int32_t num_kv_heads,
                                                   int32_t head_size,
                                                   int32_t max_seq_len,
-                                                  int32_t max_chunks);
+                                                  int32_t max_chunks,
+                                                  int32_t max_parts);
 
 /*
  * Decode attention with radix-shared prefixes computed once per group
@@ -258,15 +267,18 @@ size_t pkv_paged_attention_cascade_workspace_size(int32_t num_seqs,
  * pkv_paged_attention's with partition_size 0 (paged_attention_v1), to
  * within floating-point rounding, for any plan that follows the rules of
  * pkv_cascade_plan.  Arguments as pkv_paged_attention, PAGED5D layout.
- * Launches on `stream`: a prefix pass (one workgroup per (plan tile, KV
- * head): the tile's query rows against one chunk of the shared prefix, K/V
- * staged through LDS, partial softmax states to the workspace), then a tail
- * pass (one wavefront per (sequence, KV head): the prefix partials folded
- * in, the tokens after the prefix streamed, the output row written).  The
- * cascade kernels take 16-bit queries over caches of the same type or FP8
- * (FP8 with blocks of 16 and 32 tokens), head sizes 64 and 128, GQA groups
- * of at most 16, max_tail up to 2048 and
- * V rows aligned for 16-byte loads; other shapes run the one-pass decode of
+ * Launches two kernels on `stream`.  The first has two kinds of
+ * workgroups, running side by side: prefix work (one workgroup per (plan
+ * tile, KV head): the tile's query rows against one chunk of the shared
+ * prefix, K/V staged through LDS, partial softmax states to the workspace)
+ * and tail work (one wavefront per (tail partition, KV head): the
+ * partition's tokens streamed, its partial state to the workspace, or the
+ * output row when the sequence has no prefix and one partition).  The
+ * second merges each remaining row's states by log-sum-exp, in a fixed
+ * order, and writes the row.  The cascade kernels take 16-bit queries over
+ * caches of the same type or FP8 (FP8 with blocks of 16 and 32 tokens),
+ * head sizes 64 and 128, GQA groups of at most 16 and V rows aligned for
+ * 16-byte loads; other shapes run the one-pass decode of
  * pkv_paged_attention (the plan is then unused).
  */
 int pkv_paged_attention_cascade(void* out, const void* query,

@@ -6,7 +6,7 @@
 // sum + 1e-6, zero rows for ctx == 0 or ctx > max_seq_len.  The cascade only
 // changes where the work is done.  Sequences whose block tables begin with
 // the same blocks (a radix-shared prefix) are listed by the host in a plan
-// (CascadeParams), and two launches run:
+// (CascadeParams), and two kernels run:
 //
 // paged_cascade_kernel -- workgroups of 4 wavefronts in two roles, sized so
 //   that one of each shares a CU (LDS below half a CU's, at most 256 VGPRs
@@ -24,14 +24,17 @@
 //     on v_mfma_f32_16x16x32 over tile pairs, online softmax in the log2
 //     domain; each row's partial state (max, sum, unnormalised output) goes
 //     to the workspace slot of its (sequence, head, chunk).
-//   * Tail role (the rest): one wavefront per (sequence, KV head) item,
-//     longest tail first: the tokens after the prefix (the sequence's private
-//     tail) through the one-sequence tile pipeline.  A sequence with no
-//     prefix gets its output row written here; otherwise the tail's partial
-//     state goes to the workspace.
-// paged_cascade_merge_kernel -- one wavefront per (sequence, KV head) with a
-//   prefix: the tail state and the chunks' partial states merged by
-//   log-sum-exp, the output row written.
+//   * Tail role (the rest): one wavefront per (tail partition, KV head)
+//     item, longest partition first: the partition's tokens (after the
+//     sequence's prefix) through the one-sequence tile pipeline.  A
+//     sequence with no prefix and a single partition gets its output row
+//     written here; otherwise the partition's state goes to the workspace.
+// paged_cascade_merge_kernel -- one lane per (row, quarter of the head
+//   dimension) of the rows the tail role did not write: the row's tail
+//   partitions' and prefix chunks' states folded by log-sum-exp in that
+//   fixed order, the row written.  States cross workgroups here, so they
+//   meet at the launch boundary rather than inside the first kernel, where
+//   the merge's dependent loads would queue behind the tail's streaming.
 //
 // The log-sum-exp merge of partial states is an identity with one softmax
 // over all tokens (the final denominator is taken against the true maximum,
@@ -48,8 +51,7 @@ constexpr int kPrefixSets = 2;                                 // 16-column quer
 constexpr int kPrefixRows = kCascadeWaves * kPrefixSets * 16;  // query rows per prefix workgroup
 constexpr int kPrefixStageTiles = 2;                           // 16-token tiles per LDS stage (one pair)
 constexpr int kPrefixBuffers = 3;                              // LDS stage buffers
-constexpr int kTailBuffers = 4;                                // tile buffers per tail wavefront
-constexpr int kMergeItemsPerWorkgroup = 4;
+constexpr int kTailBuffers = 2;                                // tile buffers per tail wavefront
 
 // Largest block-table span of one prefix chunk (8-token blocks).
 constexpr int kPrefixMaxBlocks = kMaxPrefixChunk / 8;
@@ -195,6 +197,84 @@ __device__ __forceinline__ uint32_t stage_part(uint4* dst, const typename Elem<C
   return (b0 >= 0 ? 0x00ffu : 0u) | (b1 >= 0 ? 0xff00u : 0u);
 }
 
+
+// Folds one partial state (maximum m, weight sum l against it, unnormalised
+// output o of the lane's dimensions) into acc, whose m_run is its true
+// maximum.  The sum goes to the g == 0 lane of each column only: acc.l_run
+// holds per-lane parts that are summed over the column at the end.
+template <int D>
+__device__ __forceinline__ void fold_partial(WaveAcc<D>& acc, float m, float l, const float4 (&o)[Tile<D>::DT],
+                                             int g) {
+  if (m == -INFINITY) return;
+  if (m > acc.m_run) {
+    const float f = acc.m_run == -INFINITY ? 0.f : exp2f(acc.m_run - m);
+    acc.l_run *= f;
+#pragma unroll
+    for (int dt = 0; dt < Tile<D>::DT; ++dt) acc.o[dt] *= f;
+    acc.m_run = m;
+  }
+  const float w = exp2f(m - acc.m_run);
+#pragma unroll
+  for (int dt = 0; dt < Tile<D>::DT; ++dt) {
+    acc.o[dt][0] += w * o[dt].x;
+    acc.o[dt][1] += w * o[dt].y;
+    acc.o[dt][2] += w * o[dt].z;
+    acc.o[dt][3] += w * o[dt].w;
+  }
+  if (g == 0) acc.l_run += w * l;
+  acc.m_max = acc.m_run;
+}
+
+// Folds the n states of one row into acc, in order: tail partitions 0 ..
+// np-1 (ws_tail_*, slots tail0 + k), then prefix chunks (ws_*, slots
+// chunk0 + j); each lane its own row (n = 0 on lanes without one).  NB
+// states' loads are in flight at a time.
+template <int D, int NB>
+__device__ __forceinline__ void fold_states(WaveAcc<D>& acc, const CascadeParams& c, int64_t tail0, int np,
+                                            int64_t chunk0, int n, int g) {
+  constexpr int DT = Tile<D>::DT;
+  for (int j0 = 0; j0 < n; j0 += NB) {
+    float2 ml[NB];
+    float4 o[NB][DT];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      ml[b] = make_float2(-INFINITY, 0.f);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) o[b][dt] = make_float4(0.f, 0.f, 0.f, 0.f);
+      const int j = j0 + b;
+      if (j < n) {
+        const bool tail = j < np;
+        const int64_t slot = tail ? tail0 + j : chunk0 + (j - np);
+        const float* wml = tail ? c.ws_tail_ml : c.ws_ml;
+        const float* wo = (tail ? c.ws_tail_o : c.ws_o) + slot * D + 4 * g;
+        ml[b] = *reinterpret_cast<const float2*>(wml + slot * 2);
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) o[b][dt] = *reinterpret_cast<const float4*>(wo + 16 * dt);
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) fold_partial<D>(acc, ml[b].x, ml[b].y, o[b], g);
+  }
+}
+
+
+// The prefix length a sequence's rows take from the plan: 0 when the
+// sequence is not live, has no prefix, or the plan's value cannot be used
+// (not a multiple of the tile alignment, or beyond the workspace's chunks);
+// the context is then streamed whole.  The tail and merge kernels decide
+// alike.
+template <int BS>
+__device__ __forceinline__ int usable_prefix(const CascadeParams& c, int seq, bool live) {
+  constexpr int ALIGN = BS < kTile ? BS : kTile;  // a tail starts on a tile boundary of its blocks
+  const int pre = live ? c.prefix_lens[seq] : 0;
+  return (pre < 0 || pre % ALIGN != 0 || pre > c.max_chunks * c.chunk) ? 0 : pre;
+}
+
+// Tail partitions of a sequence whose tail (tokens after the prefix) is
+// `tail` tokens long: at least one, so that every sequence's row is written.
+__device__ __forceinline__ int tail_parts(const CascadeParams& c, int tail) {
+  return tail <= c.part_tokens ? 1 : (tail + c.part_tokens - 1) / c.part_tokens;
+}
 
 // Prefix role: plan tile `wi`, KV head `kvh` (see the file comment).
 template <class QT, class CT, int D, int BS>
@@ -464,95 +544,8 @@ __device__ __forceinline__ void prefix_role(const DecodeParams& p, const Cascade
   }
 }
 
-// Folds one partial state (maximum m, weight sum l against it, unnormalised
-// output o of the lane's dimensions) into acc, whose m_run is its true
-// maximum.  The sum goes to the g == 0 lane of each column only: acc.l_run
-// holds per-lane parts that are summed over the column at the end.
-template <int D>
-__device__ __forceinline__ void fold_partial(WaveAcc<D>& acc, float m, float l, const float4 (&o)[Tile<D>::DT],
-                                             int g) {
-  if (m == -INFINITY) return;
-  if (m > acc.m_run) {
-    const float f = acc.m_run == -INFINITY ? 0.f : exp2f(acc.m_run - m);
-    acc.l_run *= f;
-#pragma unroll
-    for (int dt = 0; dt < Tile<D>::DT; ++dt) acc.o[dt] *= f;
-    acc.m_run = m;
-  }
-  const float w = exp2f(m - acc.m_run);
-#pragma unroll
-  for (int dt = 0; dt < Tile<D>::DT; ++dt) {
-    acc.o[dt][0] += w * o[dt].x;
-    acc.o[dt][1] += w * o[dt].y;
-    acc.o[dt][2] += w * o[dt].z;
-    acc.o[dt][3] += w * o[dt].w;
-  }
-  if (g == 0) acc.l_run += w * l;
-  acc.m_max = acc.m_run;
-}
-
-// Folds the prefix partials of one item's heads into acc (columns col <
-// nh).  The chunks are spread over the wavefront's columns: column col takes
-// head col % nh of chunk c0 + col / nh, for as many chunks per pass as a
-// power of two of nh-column groups fits in 16, so each lane loads one
-// partial (its 4 x DT output values) and the combination runs as a tree of
-// lane exchanges (chunk c absorbs chunk c + s at step s).  row0: workspace
-// row of head 0 of the item, (seq * Hq + h0) * max_chunks.
-template <int D>
-__device__ __forceinline__ void fold_prefix(const CascadeParams& c, int64_t row0, int nh, int nch, int g, int col,
-                                            WaveAcc<D>& acc) {
-  constexpr int DT = Tile<D>::DT;
-  int per = 1;
-  while (per * 2 * nh <= 16) per *= 2;
-  const int h = col % nh, cl = col / nh;
-  const bool mine = cl < per;
-  for (int c0 = 0; c0 < nch; c0 += per) {
-    const int ch = c0 + cl;
-    const bool ok = mine && ch < nch;
-    const int64_t r = (row0 + (int64_t)h * c.max_chunks + (ok ? ch : 0));
-    const float2 ml = *reinterpret_cast<const float2*>(c.ws_ml + r * 2);
-    float4 o[DT];
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) o[dt] = *reinterpret_cast<const float4*>(c.ws_o + r * D + 16 * dt + 4 * g);
-    float m = ok ? ml.x : -INFINITY;
-    float l = ok ? ml.y : 0.f;
-    for (int st = 1; st < per; st *= 2) {
-      // Chunk cl absorbs chunk cl + st (lanes st * nh columns to the right).
-      const int src = (g << 4) + min(col + st * nh, 15);
-      const bool take = mine && (cl % (2 * st)) == 0 && cl + st < per;
-      const float pm = __shfl(m, src), pl = __shfl(l, src);
-      const float M = fmaxf(m, take ? pm : -INFINITY);
-      const float fa = (m == -INFINITY) ? 0.f : exp2f(m - M);
-      const float fb = (!take || pm == -INFINITY) ? 0.f : exp2f(pm - M);
-      l = l * fa + pl * fb;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const float4 po = make_float4(__shfl(o[dt].x, src), __shfl(o[dt].y, src), __shfl(o[dt].z, src),
-                                      __shfl(o[dt].w, src));
-        o[dt] = make_float4(o[dt].x * fa + po.x * fb, o[dt].y * fa + po.y * fb, o[dt].z * fa + po.z * fb,
-                            o[dt].w * fa + po.w * fb);
-      }
-      m = M;
-    }
-    if (col < nh) fold_partial<D>(acc, m, l, o, g);
-  }
-}
-
-
-// The prefix length a sequence's rows take from the plan: 0 when the
-// sequence is not live, has no prefix, or the plan's value cannot be used
-// (not a multiple of the tile alignment, or beyond the workspace's chunks);
-// the context is then streamed whole.  The tail and merge kernels decide
-// alike.
-template <int BS>
-__device__ __forceinline__ int usable_prefix(const CascadeParams& c, int seq, bool live) {
-  constexpr int ALIGN = BS < kTile ? BS : kTile;  // a tail starts on a tile boundary of its blocks
-  const int pre = live ? c.prefix_lens[seq] : 0;
-  return (pre < 0 || pre % ALIGN != 0 || pre > c.max_chunks * c.chunk) ? 0 : pre;
-}
-
 // Tail role: tail wavefront `tw` of `tws` takes items tw, tw + tws, ... of
-// the longest-tail-first order.
+// (tail partition, KV head unit), partitions longest first.
 template <class QT, class CT, int D, int BS>
 __device__ __forceinline__ void tail_role(const DecodeParams& p, const CascadeParams& c, int tw, int tws) {
   using QS = typename Elem<QT>::storage;
@@ -560,28 +553,33 @@ __device__ __forceinline__ void tail_role(const DecodeParams& p, const CascadePa
   using MT = typename MmaOf<QT, CT>::type;
   constexpr int KSTEPS = Tile<D>::KSTEPS;
   constexpr int DT = Tile<D>::DT;
-  constexpr int MAXT = kTailMaxTokens / kTile;
+  constexpr int MAXT = kMaxTailPart / kTile;
   using Blocks = WaveBlocks<BS, MAXT>;
   const int lane = threadIdx.x & 63;
   const int g = lane >> 4, col = lane & 15;
-  const int total = p.num_seqs * p.units;
+  const int total = c.num_parts * p.units;
   for (int rank = tw; rank < total; rank += tws) {
-    const int sr = rank / p.units;
-    const int unit = rank - sr * p.units;
-    const int seq = c.order[sr];
-    if (seq < 0 || seq >= p.num_seqs) continue;  // malformed order: the rows are not written
+    const int pi = rank / p.units;
+    const int unit = rank - pi * p.units;
+    const int2 part = c.parts[pi];
+    const int seq = part.x, k = part.y;
+    if (seq < 0 || seq >= p.num_seqs) continue;  // malformed entry: nothing is written
     int kvh, h0, nh;
     unit_heads(p, unit, kvh, h0, nh);
     const uint32_t ctx = (uint32_t)p.context_lens[seq];
     const bool live = ctx != 0 && ctx <= (uint32_t)p.max_seq_len;
     const int pre = usable_prefix<BS>(c, seq, live);
-    const int t0 = min(pre, (int)ctx);
-    const int t1 = min((int)ctx, t0 + kTailMaxTokens);
+    const int tstart = live ? min(pre, (int)ctx) : 0;
+    const int np = tail_parts(c, live ? (int)ctx - tstart : 0);
+    if (k < 0 || k >= np || k >= c.max_parts) continue;
+    const int t0 = tstart + k * c.part_tokens;
+    const int t1 = live ? min((int)ctx, t0 + c.part_tokens) : t0;
+    const bool direct = pre == 0 && np == 1;  // the row is this partition's
 
     Blocks blk;
     const int lb0 = t0 / BS;
     blk.load(p.block_tables + (int64_t)seq * p.max_blocks_per_seq, p.num_blocks,
-             live ? (t1 + BS - 1) / BS - lb0 : 0, lb0, t0, 0, 1, lane);
+             t1 > t0 ? (t1 + BS - 1) / BS - lb0 : 0, lb0, t0, 0, 1, lane);
     uint4 qa[KSTEPS];
     uint4 qb[1];
     load_query<QT, MT, D, WideFp8<CT, D>::value>(p, seq, h0, nh, g, col, qa, qb);
@@ -589,7 +587,7 @@ __device__ __forceinline__ void tail_role(const DecodeParams& p, const CascadePa
 
     WaveAcc<D> acc;
     acc.init();
-    if (live && t1 > t0) {
+    if (t1 > t0) {
       const CS* kbase = static_cast<const CS*>(p.k_cache) + (int64_t)kvh * p.k_head_stride;
       const CS* vbase = static_cast<const CS*>(p.v_cache) + (int64_t)kvh * p.v_head_stride;
       stream_tiles<QT, CT, D, BS, 1, MAXT, kTailBuffers>(p, kbase, vbase, blk, t0, t1, ctx, 0, g, col, qa, qb, slope,
@@ -602,24 +600,26 @@ __device__ __forceinline__ void tail_role(const DecodeParams& p, const CascadePa
       for (int dt = 0; dt < DT; ++dt) acc.o[dt] *= f;
     }
     const float L = column_sum(acc.l_run);
-    if (col >= nh) continue;
     const int64_t row = (int64_t)seq * p.num_heads + h0 + col;
-    if (pre > 0) {
-      // The merge kernel finishes the row: the tail's state, as a partial.
-      float* wo = c.ws_tail_o + row * D;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt)
-        *reinterpret_cast<float4*>(wo + 16 * dt + 4 * g) =
-            make_float4(acc.o[dt][0], acc.o[dt][1], acc.o[dt][2], acc.o[dt][3]);
-      if (g == 0) *reinterpret_cast<float2*>(c.ws_tail_ml + row * 2) = make_float2(acc.m_max, L);
-    } else {
+    if (direct) {
+      if (col >= nh) continue;
       const float inv = live ? p.v_scale / (L + 1e-6f) : 0.f;
       QS* out = static_cast<QS*>(p.out) + row * D;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt)
         store4<QT>(out + 16 * dt + 4 * g, acc.o[dt][0] * inv, acc.o[dt][1] * inv, acc.o[dt][2] * inv,
                    acc.o[dt][3] * inv);
+      continue;
     }
+    // This partition's state, for the merge kernel.
+    if (col >= nh) continue;
+    const int64_t slot = row * c.max_parts + k;
+    float* wo = c.ws_tail_o + slot * D;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+      *reinterpret_cast<float4*>(wo + 16 * dt + 4 * g) =
+          make_float4(acc.o[dt][0], acc.o[dt][1], acc.o[dt][2], acc.o[dt][3]);
+    if (g == 0) *reinterpret_cast<float2*>(c.ws_tail_ml + slot * 2) = make_float2(acc.m_max, L);
   }
 }
 
@@ -649,58 +649,49 @@ __global__ __launch_bounds__(64 * kCascadeWaves, 2) void paged_cascade_kernel(De
   }
 }
 
-// One wavefront per (sequence, KV head) item with a prefix: the tail state
-// and the prefix chunks' states folded into one softmax, the row written.
+// Rows of 16 per wavefront (one wavefront per workgroup); lane (col, g)
+// takes quarter g of row 16 * blockIdx.x + col.
 template <class QT, int D, int BS>
-__global__ __launch_bounds__(64 * kMergeItemsPerWorkgroup) void paged_cascade_merge_kernel(DecodeParams p,
-                                                                                          CascadeParams c) {
+__global__ __launch_bounds__(64) void paged_cascade_merge_kernel(DecodeParams p, CascadeParams c) {
   using QS = typename Elem<QT>::storage;
-  constexpr int DT = Tile<D>::DT;
-  const int lane = threadIdx.x & 63;
+  constexpr int kStates = 6;  // states whose loads are in flight together
+  const int lane = threadIdx.x;
   const int g = lane >> 4, col = lane & 15;
-  const int item = (int)blockIdx.x * kMergeItemsPerWorkgroup + (int)(threadIdx.x >> 6);
-  if (item >= p.num_seqs * p.units) return;
-  const int seq = item / p.units;
-  int kvh, h0, nh;
-  unit_heads(p, item - seq * p.units, kvh, h0, nh);
+  const int64_t row = (int64_t)blockIdx.x * 16 + col;
+  bool on = row < (int64_t)p.num_seqs * p.num_heads;
+  const int seq = on ? (int)(row / p.num_heads) : 0;
   const uint32_t ctx = (uint32_t)p.context_lens[seq];
   const bool live = ctx != 0 && ctx <= (uint32_t)p.max_seq_len;
   const int pre = usable_prefix<BS>(c, seq, live);
-  if (pre == 0) return;  // written by the tail role
+  const int np = tail_parts(c, live ? (int)ctx - min(pre, (int)ctx) : 0);
+  on = on && !(pre == 0 && np == 1);  // rows the tail role wrote
+  const int nt = min(np, c.max_parts);
+  const int nch = pre > 0 ? (pre + c.chunk - 1) / c.chunk : 0;
   WaveAcc<D> acc;
   acc.init();
-  if (col < nh) {
-    const int64_t row = (int64_t)seq * p.num_heads + h0 + col;
-    const float2 ml = *reinterpret_cast<const float2*>(c.ws_tail_ml + row * 2);
-    float4 o[DT];
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) o[dt] = *reinterpret_cast<const float4*>(c.ws_tail_o + row * D + 16 * dt + 4 * g);
-    fold_partial<D>(acc, ml.x, ml.y, o, g);
-  }
-  fold_prefix<D>(c, ((int64_t)seq * p.num_heads + h0) * c.max_chunks, nh, (pre + c.chunk - 1) / c.chunk, g, col, acc);
+  fold_states<D, kStates>(acc, c, row * c.max_parts, nt, row * c.max_chunks, on ? nt + nch : 0, g);
   const float L = column_sum(acc.l_run);
-  if (col >= nh) return;
+  if (!on) return;
   const float inv = p.v_scale / (L + 1e-6f);
-  QS* out = static_cast<QS*>(p.out) + ((int64_t)seq * p.num_heads + h0 + col) * D;
+  QS* out = static_cast<QS*>(p.out) + row * D;
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
+  for (int dt = 0; dt < Tile<D>::DT; ++dt)
     store4<QT>(out + 16 * dt + 4 * g, acc.o[dt][0] * inv, acc.o[dt][1] * inv, acc.o[dt][2] * inv, acc.o[dt][3] * inv);
 }
 
 template <class QT, class CT, int D, int BS>
 static hipError_t launch_cascade_bs(const DecodeParams& p, const CascadeParams& c, hipStream_t stream) {
-  const int64_t items = (int64_t)p.num_seqs * p.units;
   const int64_t prefix_wgs = (int64_t)c.num_tiles * p.num_kv_heads;
-  // One tail wavefront per item; the hardware deals the tail workgroups to
-  // CUs as slots free up, longest tails first.
-  const int64_t tail_wgs = (items + kCascadeWaves - 1) / kCascadeWaves;
+  // One tail wavefront per (partition, unit) item; the hardware deals the
+  // tail workgroups to CUs as slots free up, longest partitions first.
+  const int64_t tail_wgs = ((int64_t)c.num_parts * p.units + kCascadeWaves - 1) / kCascadeWaves;
   hipLaunchKernelGGL((paged_cascade_kernel<QT, CT, D, BS>), dim3((unsigned)(prefix_wgs + tail_wgs)),
                      dim3(64 * kCascadeWaves), 0, stream, p, c);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess || c.num_tiles == 0) return e;
-  hipLaunchKernelGGL((paged_cascade_merge_kernel<QT, D, BS>),
-                     dim3((unsigned)((items + kMergeItemsPerWorkgroup - 1) / kMergeItemsPerWorkgroup)),
-                     dim3(64 * kMergeItemsPerWorkgroup), 0, stream, p, c);
+  if (e != hipSuccess) return e;
+  const int64_t rows = (int64_t)p.num_seqs * p.num_heads;
+  hipLaunchKernelGGL((paged_cascade_merge_kernel<QT, D, BS>), dim3((unsigned)((rows + 15) / 16)), dim3(64), 0, stream,
+                     p, c);
   return hipGetLastError();
 }
 

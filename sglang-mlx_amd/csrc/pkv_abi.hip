@@ -129,13 +129,13 @@ DecodeWorkspace decode_workspace_layout(int32_t num_seqs, int32_t num_heads, int
   return w;
 }
 CascadeWorkspace cascade_workspace_layout(int32_t num_seqs, int32_t num_heads, int32_t head_size,
-                                          int32_t max_chunks) {
+                                          int32_t max_chunks, int32_t max_parts) {
   CascadeWorkspace w;
   auto align = [](size_t x) { return (x + 255) & ~size_t(255); };
   w.ml_bytes = align((size_t)num_seqs * num_heads * max_chunks * 2 * sizeof(float));
   w.o_bytes = align((size_t)num_seqs * num_heads * max_chunks * head_size * sizeof(float));
-  w.tail_ml_bytes = align((size_t)num_seqs * num_heads * 2 * sizeof(float));
-  w.tail_o_bytes = align((size_t)num_seqs * num_heads * head_size * sizeof(float));
+  w.tail_ml_bytes = align((size_t)num_seqs * num_heads * max_parts * 2 * sizeof(float));
+  w.tail_o_bytes = align((size_t)num_seqs * num_heads * max_parts * head_size * sizeof(float));
   w.total = w.ml_bytes + w.o_bytes + w.tail_ml_bytes + w.tail_o_bytes;
   return w;
 }
@@ -224,10 +224,11 @@ size_t pkv_paged_attention_workspace_size(int32_t num_seqs, int32_t num_heads, i
 }
 
 size_t pkv_paged_attention_cascade_workspace_size(int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
-                                                  int32_t head_size, int32_t max_seq_len, int32_t max_chunks) {
+                                                  int32_t head_size, int32_t max_seq_len, int32_t max_chunks,
+                                                  int32_t max_parts) {
   const size_t v1 = pkv_paged_attention_workspace_size(num_seqs, num_heads, num_kv_heads, head_size, max_seq_len, 0);
-  if (v1 == 0 || max_chunks <= 0 || max_chunks > 65536) return 0;
-  return std::max(v1, pkv::cascade_workspace_layout(num_seqs, num_heads, head_size, max_chunks).total);
+  if (v1 == 0 || max_chunks <= 0 || max_chunks > 65536 || max_parts <= 0 || max_parts > 65536) return 0;
+  return std::max(v1, pkv::cascade_workspace_layout(num_seqs, num_heads, head_size, max_chunks, max_parts).total);
 }
 
 }  // extern "C"
@@ -327,10 +328,12 @@ int paged_attention_impl(void* out, const void* query, const void* key_cache, co
       (v_head_stride * cb) % v_align != 0)
     return fail(PKV_ERR_INVALID, "cache base or strides are not aligned for vector loads");
   if (plan != nullptr) {
-    if (plan->prefix_lens == nullptr || plan->order == nullptr)
-      return fail(PKV_ERR_INVALID, "cascade plan: prefix_lens and order are required");
-    if (plan->num_tiles < 0 || plan->num_members < 0)
-      return fail(PKV_ERR_INVALID, "cascade plan: num_tiles and num_members must be non-negative");
+    if (plan->prefix_lens == nullptr || plan->parts == nullptr)
+      return fail(PKV_ERR_INVALID, "cascade plan: prefix_lens and parts are required");
+    if (plan->num_tiles < 0 || plan->num_members < 0 || plan->num_parts < 0)
+      return fail(PKV_ERR_INVALID, "cascade plan: num_tiles, num_members and num_parts must be non-negative");
+    if (reinterpret_cast<uintptr_t>(plan->parts) % 8 != 0)
+      return fail(PKV_ERR_INVALID, "cascade plan: parts must be 8-byte aligned");
     if (plan->num_tiles > 0 && (plan->members == nullptr || plan->tiles == nullptr || plan->num_members == 0))
       return fail(PKV_ERR_INVALID, "cascade plan: tiles need members");
     if (plan->tiles != nullptr && !aligned16(plan->tiles))
@@ -339,23 +342,27 @@ int paged_attention_impl(void* out, const void* query, const void* key_cache, co
         plan->chunk_tokens > pkv::kMaxPrefixChunk)
       return fail(PKV_ERR_INVALID, "cascade plan: chunk_tokens must be a positive multiple of 16 and of block_size, "
                                    "at most 4096");
-    if (plan->max_chunks <= 0 || plan->max_chunks > 65536 || plan->max_tail < 0)
-      return fail(PKV_ERR_INVALID, "cascade plan: max_chunks must be in [1, 65536] and max_tail non-negative");
-    if ((int64_t)num_seqs * num_heads * plan->max_chunks * head_size > ((int64_t)1 << 40))
+    if (plan->part_tokens <= 0 || plan->part_tokens % pkv::kTile != 0 || plan->part_tokens % block_size != 0 ||
+        plan->part_tokens > pkv::kMaxTailPart)
+      return fail(PKV_ERR_INVALID, "cascade plan: part_tokens must be a positive multiple of 16 and of block_size, "
+                                   "at most 1024");
+    if (plan->max_chunks <= 0 || plan->max_chunks > 65536 || plan->max_parts <= 0 || plan->max_parts > 65536)
+      return fail(PKV_ERR_INVALID, "cascade plan: max_chunks and max_parts must be in [1, 65536]");
+    if ((int64_t)num_seqs * num_heads * (plan->max_chunks + plan->max_parts) * head_size > ((int64_t)1 << 40))
       return fail(PKV_ERR_UNSUPPORTED, "cascade plan: workspace beyond 4 TiB");
   }
   // The cascade kernels: 16-bit queries over caches of the same type or
-  // FP8, head sizes 64 and 128, GQA groups of at most 16, tails of at most
-  // kTailMaxTokens, and V rows aligned for 16-byte loads.  Other shapes take
-  // the one-pass decode below, whose result is the same.
+  // FP8, head sizes 64 and 128, GQA groups of at most 16, and V rows aligned
+  // for 16-byte loads.  Other shapes take the one-pass decode below, whose
+  // result is the same.
   const bool cascade = plan != nullptr && !rows && (q_dtype == PKV_BF16 || q_dtype == PKV_F16) &&
                        (cache_dtype == q_dtype || (fp8 && block_size >= 16)) &&
                        (head_size == 64 || head_size == 128) &&
-                       num_heads / num_kv_heads <= 16 && plan->max_tail <= pkv::kTailMaxTokens &&
+                       num_heads / num_kv_heads <= 16 &&
                        aligned16(value_cache) && (vbs * cb) % 16 == 0 && (v_head_stride * cb) % 16 == 0;
   const pkv::DecodeWorkspace w = pkv::decode_workspace_layout(num_seqs, num_heads, head_size, parts);
   const pkv::CascadeWorkspace cw =
-      plan != nullptr ? pkv::cascade_workspace_layout(num_seqs, num_heads, head_size, plan->max_chunks)
+      plan != nullptr ? pkv::cascade_workspace_layout(num_seqs, num_heads, head_size, plan->max_chunks, plan->max_parts)
                       : pkv::CascadeWorkspace{0, 0, 0, 0, 0};
   if (cascade && (workspace == nullptr || workspace_bytes < cw.total))
     return fail(PKV_ERR_INVALID, "workspace is smaller than pkv_paged_attention_cascade_workspace_size()");
@@ -425,9 +432,9 @@ int paged_attention_impl(void* out, const void* query, const void* key_cache, co
   if (cascade) {
     pkv::CascadeParams c;
     c.prefix_lens = plan->prefix_lens;
-    c.order = plan->order;
     c.members = plan->members;
     c.tiles = reinterpret_cast<const int4*>(plan->tiles);
+    c.parts = reinterpret_cast<const int2*>(plan->parts);
     c.ws_ml = reinterpret_cast<float*>(ws);
     c.ws_o = reinterpret_cast<float*>(ws + cw.ml_bytes);
     c.ws_tail_ml = reinterpret_cast<float*>(ws + cw.ml_bytes + cw.o_bytes);
@@ -436,7 +443,9 @@ int paged_attention_impl(void* out, const void* query, const void* key_cache, co
     c.num_tiles = plan->num_tiles;
     c.chunk = plan->chunk_tokens;
     c.max_chunks = plan->max_chunks;
-    c.max_tail = plan->max_tail;
+    c.num_parts = plan->num_parts;
+    c.part_tokens = plan->part_tokens;
+    c.max_parts = plan->max_parts;
     if (q_dtype == PKV_BF16)
       e = fp8 ? pkv::launch_cascade_typed<pkv::BF16, pkv::FP8>(p, c, head_size, block_size, s, &ok)
               : pkv::launch_cascade_typed<pkv::BF16, pkv::BF16>(p, c, head_size, block_size, s, &ok);

@@ -104,35 +104,43 @@ struct DecodeParams {
 // the block tables (see include/pagedkv.h, pkv_cascade_plan):
 //   prefix_lens[s]: leading tokens of sequence s that the prefix pass covers
 //                   (0: none), a multiple of the block size and of 16;
-//   order[r]:       the sequences by descending tail length (a permutation);
 //   members[i]:     sequence ids, the members of each prefix group adjacent;
 //   tiles[w]:       (member_begin, member_count, token_begin, token_end) of
 //                   prefix-pass work unit w: members[member_begin ..
 //                   +member_count) share the blocks of the first one's table
 //                   over tokens [0, token_end), and the unit covers tokens
-//                   [token_begin, token_end) = chunk token_begin / chunk.
+//                   [token_begin, token_end) = chunk token_begin / chunk;
+//   parts[r]:       (sequence, k) of tail partition r, longest first:
+//                   partition k of a sequence covers tokens
+//                   [pre + k * part_tokens, min(ctx, pre + (k + 1) *
+//                   part_tokens)) after its prefix pre, and a sequence has
+//                   max(1, ceil((ctx - pre) / part_tokens)) of them.
 // Partial softmax states of the prefix pass, per (sequence, query head,
 // chunk): (max, sum) in ws_ml and the unnormalised output in ws_o; of the
-// tail pass, per (sequence, query head), in ws_tail_ml / ws_tail_o.
+// tail pass, per (sequence, query head, partition), in ws_tail_ml /
+// ws_tail_o.  A sequence with no prefix and one partition has its rows
+// written by the tail pass; the merge kernel writes the others.
 struct CascadeParams {
   const int32_t* prefix_lens;
-  const int32_t* order;
   const int32_t* members;
   const int4* tiles;
+  const int2* parts;
   float* ws_ml;       // [B, Hq, max_chunks, 2]
   float* ws_o;        // [B, Hq, max_chunks, D]
-  float* ws_tail_ml;  // [B, Hq, 2]
-  float* ws_tail_o;   // [B, Hq, D]
+  float* ws_tail_ml;  // [B, Hq, max_parts, 2]
+  float* ws_tail_o;   // [B, Hq, max_parts, D]
   int32_t num_members;
   int32_t num_tiles;
+  int32_t num_parts;
   int32_t chunk;       // tokens per chunk: a multiple of 16 and of the block size, at most kMaxPrefixChunk
   int32_t max_chunks;  // chunk slots per (sequence, query head) in the workspace
-  int32_t max_tail;    // longest context after the prefix
+  int32_t part_tokens; // tokens per tail partition: a multiple of 16 and of the block size, at most kMaxTailPart
+  int32_t max_parts;   // partition slots per (sequence, query head) in the workspace
 };
 constexpr int kMaxPrefixChunk = 4096;
-// Longest tail (tokens after the prefix) of the cascade's tail kernel: each
-// wavefront keeps its item's block ids in registers.
-constexpr int kTailMaxTokens = 2048;
+// Longest tail partition: each wavefront keeps its partition's block ids in
+// registers.
+constexpr int kMaxTailPart = 1024;
 // Defined in cascade_impl.h for the (query, cache) pairs (BF16, BF16),
 // (F16, F16), (BF16, FP8) and (F16, FP8); *ok is cleared for a shape the
 // cascade kernels do not cover (the caller then runs the one-pass decode).
@@ -143,7 +151,7 @@ struct CascadeWorkspace {
   size_t ml_bytes, o_bytes, tail_ml_bytes, tail_o_bytes, total;
 };
 CascadeWorkspace cascade_workspace_layout(int32_t num_seqs, int32_t num_heads, int32_t head_size,
-                                          int32_t max_chunks);
+                                          int32_t max_chunks, int32_t max_parts);
 
 // Scratch carve-up shared by the size query and the launcher: per-partition
 // (max, sum) pairs, then per-partition outputs.

@@ -191,22 +191,24 @@ def _plan_struct(plan, B: int, dev: torch.device):
     """The ctypes pkv_cascade_plan of a CascadePlan (checked: int32 tensors
     on the query's device, contiguous, with the shapes the header states)."""
     arrays = {}
-    for name, shape in (("prefix_lens", (B,)), ("order", (B,)), ("members", None), ("tiles", None)):
+    for name, shape in (("prefix_lens", (B,)), ("members", None), ("tiles", None), ("parts", None)):
         t = getattr(plan, name)
         if not isinstance(t, torch.Tensor) or t.dtype != torch.int32 or t.device != dev or not t.is_contiguous():
             raise ValueError(f"cascade plan: {name} must be a contiguous int32 tensor on {dev}")
         if shape is not None and tuple(t.shape) != shape:
             raise ValueError(f"cascade plan: {name} must have shape {list(shape)}")
         arrays[name] = t
-    tiles = arrays["tiles"]
+    tiles, parts = arrays["tiles"], arrays["parts"]
     if tiles.dim() != 2 or tiles.shape[1] != 4:
         raise ValueError("cascade plan: tiles must have shape [num_tiles, 4]")
+    if parts.dim() != 2 or parts.shape[1] != 2:
+        raise ValueError("cascade plan: parts must have shape [num_parts, 2]")
     if arrays["members"].dim() != 1:
         raise ValueError("cascade plan: members must be 1-D")
     ptr = lambda t: t.data_ptr() if t.numel() else None  # noqa: E731
-    return _lib.CascadePlanC(ptr(arrays["prefix_lens"]), ptr(arrays["order"]), ptr(arrays["members"]), ptr(tiles),
-                             arrays["members"].numel(), tiles.shape[0], int(plan.chunk_tokens),
-                             int(plan.max_chunks), int(plan.max_tail))
+    return _lib.CascadePlanC(ptr(arrays["prefix_lens"]), ptr(arrays["members"]), ptr(tiles), ptr(parts),
+                             arrays["members"].numel(), tiles.shape[0], parts.shape[0], int(plan.chunk_tokens),
+                             int(plan.max_chunks), int(plan.part_tokens), int(plan.max_parts))
 
 
 def _paged_attention(op, query, key_cache, value_cache, block_tables, context_lens, num_kv_heads,
@@ -241,17 +243,17 @@ def _paged_attention(op, query, key_cache, value_cache, block_tables, context_le
         with torch.cuda.device(dev):
             stream = _stream(dev)
             need = lib.pkv_paged_attention_cascade_workspace_size(B, Hq, num_kv_heads, D, max_seq_len,
-                                                                  int(plan.max_chunks))
+                                                                  int(plan.max_chunks), int(plan.max_parts))
             if need == 0:
-                raise ValueError("cascade plan: invalid sizes (max_chunks must be in [1, 65536])")
+                raise ValueError("cascade plan: invalid sizes (max_chunks and max_parts must be in [1, 65536])")
             ws = _decode_scratch(dev, stream, need)
             st = lib.pkv_paged_attention_cascade(
                 out.data_ptr(), query.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
                 bt.data_ptr(), lens.data_ptr(), None if alibi is None else alibi.data_ptr(), ctypes.byref(cplan),
                 B, Hq, num_kv_heads, D, block_size, bt.shape[1], max_seq_len, key_cache.shape[0],
                 float(scale), query.stride(0), key_cache.stride(0), key_cache.stride(1),
-                value_cache.stride(0), value_cache.stride(1), ws.data_ptr(), ws.numel(), qc, cc, k_scale, v_scale,
-                stream)
+                value_cache.stride(0), value_cache.stride(1), ws.data_ptr(), ws.numel(), qc, cc, k_scale,
+                v_scale, stream)
         _lib.check(st)
         return out
     with torch.cuda.device(dev):

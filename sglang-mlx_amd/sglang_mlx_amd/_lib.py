@@ -37,14 +37,16 @@ class CascadePlanC(ctypes.Structure):
 
     _fields_ = [
         ("prefix_lens", _c_void_p),
-        ("order", _c_void_p),
         ("members", _c_void_p),
         ("tiles", _c_void_p),
+        ("parts", _c_void_p),
         ("num_members", _i32),
         ("num_tiles", _i32),
+        ("num_parts", _i32),
         ("chunk_tokens", _i32),
         ("max_chunks", _i32),
-        ("max_tail", _i32),
+        ("part_tokens", _i32),
+        ("max_parts", _i32),
     ]
 
 
@@ -74,7 +76,7 @@ SIGNATURES = {
         _i32, _i32,                                               # q dtype, cache dtype
         _f32, _f32, _c_void_p,                                    # k_scale, v_scale (FP8), stream
     ]),
-    "pkv_paged_attention_cascade_workspace_size": (_size, [_i32, _i32, _i32, _i32, _i32, _i32]),
+    "pkv_paged_attention_cascade_workspace_size": (_size, [_i32, _i32, _i32, _i32, _i32, _i32, _i32]),
     "pkv_paged_attention_cascade": (ctypes.c_int, [
         _c_void_p, _c_void_p, _c_void_p, _c_void_p,              # out, q, kc, vc
         _c_void_p, _c_void_p, _c_void_p,                          # block_tables, ctx, alibi

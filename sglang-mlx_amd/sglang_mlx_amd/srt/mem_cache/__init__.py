@@ -9,12 +9,12 @@ from .evict_policy import (EvictionStrategy, FIFOStrategy, FILOStrategy, LFUStra
                            PriorityStrategy)
 from .memory_pool import MHATokenPool, PooledKVCache, TokenPoolAllocator, decode_batch
 from .paged_pool import (BlockAllocator, BlockRadixCache, BlockTable, CascadePlan, build_block_tables,
-                         build_cascade_plan, plan_prefix_groups)
+                         build_cascade_plan, plan_prefix_groups, tail_partitions)
 from .radix_cache import RadixCache, TreeNode
 
 __all__ = [
     "BasePrefixCache", "BlockAllocator", "BlockRadixCache", "BlockTable", "build_block_tables", "build_cascade_plan",
-    "CascadePlan", "plan_prefix_groups", "CacheInitParams", "EvictParams", "EvictResult", "EvictionStrategy", "FIFOStrategy",
+    "CascadePlan", "plan_prefix_groups", "tail_partitions", "CacheInitParams", "EvictParams", "EvictResult", "EvictionStrategy", "FIFOStrategy",
     "FILOStrategy", "InsertParams", "InsertResult", "LFUStrategy", "LRUStrategy", "MHATokenPool", "MRUStrategy",
     "MatchResult", "PooledKVCache", "PriorityStrategy", "decode_batch", "RadixCache", "TokenPoolAllocator", "TreeNode",
 ]

@@ -23,6 +23,10 @@ tables, so this module keeps the same structures at block granularity:
   tuple of one block's token ids and the value is the block id, so a prefix
   match returns the blocks that hold it.  The tree holds its own reference
   to every block it caches; eviction drops it.
+* plan_prefix_groups / build_cascade_plan -- the shared-prefix plan of
+  paged_attention_cascade: groups of sequences whose tables begin with the
+  same blocks, the prefix pass's work units over them, and the tail
+  partitions (tail_partitions) of the tokens after each prefix.
 """
 
 from __future__ import annotations
@@ -178,6 +182,8 @@ def build_block_tables(tables: list[BlockTable], max_blocks: int | None = None) 
 PREFIX_ROWS = 128          # query rows of one prefix-pass workgroup
 PREFIX_MAX_CHUNK = 4096    # longest prefix chunk of one prefix-pass workgroup
 PREFIX_MIN_CHUNK = 256
+TAIL_PART = 512            # default tokens per tail partition
+TAIL_MAX_PART = 1024       # longest tail partition of the tail pass
 
 
 @dataclass
@@ -187,12 +193,13 @@ class CascadePlan:
     host-side (members, prefix tokens) of each group for inspection."""
 
     prefix_lens: "torch.Tensor"
-    order: "torch.Tensor"
     members: "torch.Tensor"
     tiles: "torch.Tensor"
+    parts: "torch.Tensor"
     chunk_tokens: int
     max_chunks: int
-    max_tail: int
+    part_tokens: int
+    max_parts: int
     groups: list = field(default_factory=list)
 
 
@@ -231,16 +238,35 @@ def plan_prefix_groups(block_tables: np.ndarray, context_lens: np.ndarray, block
     return groups
 
 
+def tail_partitions(tails: np.ndarray, part_tokens: int) -> np.ndarray:
+    """The tail partitions [(sequence, k)] of sequences whose tails (tokens
+    after the prefix) are ``tails``: max(1, ceil(tail / part_tokens)) per
+    sequence, partition k holding tokens [k * part_tokens, min(tail, (k + 1)
+    * part_tokens)) of the tail; longest partitions first, then by sequence
+    and k.  int32 [num_parts, 2]."""
+    tails = np.maximum(np.asarray(tails, dtype=np.int64), 0)
+    n = np.maximum(1, -(-tails // part_tokens))
+    seq = np.repeat(np.arange(tails.size, dtype=np.int64), n)
+    k = np.arange(seq.size, dtype=np.int64) - np.repeat(np.cumsum(n) - n, n)
+    length = np.minimum(part_tokens, tails[seq] - k * part_tokens)
+    order = np.lexsort((k, seq, -length))
+    return np.stack([seq[order], k[order]], axis=1).astype(np.int32)
+
+
 def build_cascade_plan(block_tables: np.ndarray, context_lens: np.ndarray, block_size: int, num_heads: int,
                        num_kv_heads: int, device=None, num_cus: int = 256, min_members: int = 2,
-                       min_shared_tokens: int = 0, chunk_tokens: int | None = None) -> CascadePlan:
+                       min_shared_tokens: int = 0, chunk_tokens: int | None = None,
+                       part_tokens: int | None = None) -> CascadePlan:
     """The paged_attention_cascade plan of a batch from its host-side int32
     block tables [B, max_blocks] and context lengths [B]
     (build_block_tables' output).  Work units of the prefix pass are
     (up to 128 // group members of a group) x (one chunk of its prefix);
     the chunk is the longest power of two in [256, 4096] tokens (a multiple
     of block_size and 16) that still gives every one of ``num_cus`` CUs a
-    workgroup (units x KV heads), unless ``chunk_tokens`` fixes it."""
+    workgroup (units x KV heads), unless ``chunk_tokens`` fixes it.  The
+    tokens after each sequence's prefix are cut into tail partitions of
+    ``part_tokens`` (default TAIL_PART tokens), so that no tail wavefront
+    streams much more than the others."""
     import torch
 
     bt = np.asarray(block_tables, dtype=np.int32)
@@ -266,6 +292,12 @@ def build_cascade_plan(block_tables: np.ndarray, context_lens: np.ndarray, block
         chunk = int(chunk_tokens)
         if chunk <= 0 or chunk % step or chunk > PREFIX_MAX_CHUNK:
             raise ValueError("chunk_tokens must be a positive multiple of 16 and of block_size, at most 4096")
+    if part_tokens is None:
+        part = max(step, TAIL_PART - TAIL_PART % step)
+    else:
+        part = int(part_tokens)
+        if part <= 0 or part % step or part > TAIL_MAX_PART:
+            raise ValueError("part_tokens must be a positive multiple of 16 and of block_size, at most 1024")
     prefix_lens = np.zeros(B, dtype=np.int32)
     members, tiles = [], []
     max_chunks = 1
@@ -280,17 +312,18 @@ def build_cascade_plan(block_tables: np.ndarray, context_lens: np.ndarray, block
             for c in range(nch):
                 tiles.append((base + m0, mc, c * chunk, min(p, (c + 1) * chunk)))
     tail = np.maximum(ctx - prefix_lens, 0)
-    order = np.argsort(-tail, kind="stable").astype(np.int32)
+    parts = tail_partitions(tail, part)
+    max_parts = int(max(1, -(-int(tail.max()) // part))) if B else 1
     dev = torch.device(device) if device is not None else torch.device("cpu")
 
     def t(a, shape=None):
         x = torch.as_tensor(np.asarray(a, dtype=np.int32).reshape(shape) if shape else np.asarray(a, dtype=np.int32))
         return x.to(dev)
 
-    return CascadePlan(prefix_lens=t(prefix_lens), order=t(order), members=t(members),
+    return CascadePlan(prefix_lens=t(prefix_lens), members=t(members),
                        tiles=t(tiles if tiles else np.zeros((0, 4), dtype=np.int32), (-1, 4)),
-                       chunk_tokens=chunk, max_chunks=max_chunks, max_tail=int(tail.max()) if B else 0,
-                       groups=groups)
+                       parts=t(parts, (-1, 2)), chunk_tokens=chunk, max_chunks=max_chunks, part_tokens=part,
+                       max_parts=max_parts, groups=groups)
 
 
 class BlockRadixCache:

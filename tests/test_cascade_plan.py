@@ -3,31 +3,33 @@ plan_prefix_groups (CPU only).
 
 * Known answers on hand-made block tables: grouping by first block, the
   longest common run of leading blocks held in full by every member, groups
-  of one and short prefixes dropped, tiles, chunk choice, tail order.
+  of one and short prefixes dropped, tiles, chunk choice, tail partitions
+  and their order.
 * Invariants on random radix-shaped batches: every member maps the group's
   prefix to the first member's blocks; the tiles of a group cover its prefix
   [0, P) chunk by chunk for every member exactly once; member counts fit 128
-  query rows; order is a permutation by descending tail.
+  query rows; the tail partitions cover every sequence's tail [P, ctx)
+  exactly once (one empty partition for an empty tail), longest first.
 * The plan's meaning, restated in float64 with the oracle's partial
   softmax states: per tile, the member rows against the first member's
-  blocks over [token_begin, token_end); per sequence, the tail
-  [prefix, ctx) over its own blocks; all merged by log-sum-exp.  This equals
-  the oracle's paged_attention to float64 rounding on random batches, and a
+  blocks over [token_begin, token_end); per tail partition, its tokens over
+  the sequence's own blocks; all merged by log-sum-exp.  This equals the
+  oracle's paged_attention to float64 rounding on random batches, and a
   planted mistake in a plan (a prefix one block short, a member left out
-  of its tiles) makes it differ.
+  of its tiles, a tail partition left out) makes it differ.
 """
 
 import numpy as np
 import pytest
 
 from oracle import pagedkv_oracle as orc
-from sglang_mlx_amd.srt.mem_cache import build_cascade_plan, plan_prefix_groups
+from sglang_mlx_amd.srt.mem_cache import build_cascade_plan, plan_prefix_groups, tail_partitions
 
 
 def np_plan(plan):
-    return dict(prefix_lens=plan.prefix_lens.numpy(), order=plan.order.numpy(), members=plan.members.numpy(),
-                tiles=plan.tiles.numpy(), chunk=plan.chunk_tokens, max_chunks=plan.max_chunks,
-                max_tail=plan.max_tail)
+    return dict(prefix_lens=plan.prefix_lens.numpy(), members=plan.members.numpy(), tiles=plan.tiles.numpy(),
+                parts=plan.parts.numpy(), chunk=plan.chunk_tokens, max_chunks=plan.max_chunks,
+                part_tokens=plan.part_tokens, max_parts=plan.max_parts)
 
 
 def test_groups_known_answers():
@@ -60,15 +62,27 @@ def test_plan_known_answers():
     assert p["prefix_lens"].tolist() == [32, 32, 32, 0, 0]
     assert p["members"].tolist() == [0, 1, 2]
     assert p["tiles"].tolist() == [[0, 3, 0, 32]]
-    assert p["chunk"] == 256 and p["max_chunks"] == 1 and p["max_tail"] == 32
-    # tails 8, 32, 18, 20, 10 -> longest first, ties by index
-    assert p["order"].tolist() == [1, 3, 2, 4, 0]
-    p = np_plan(build_cascade_plan(bt, ctx, 16, 32, 8, chunk_tokens=16))
+    assert p["chunk"] == 256 and p["max_chunks"] == 1
+    # tails 8, 32, 18, 20, 10: one partition each, longest first, ties by index
+    assert p["part_tokens"] == 512 and p["max_parts"] == 1
+    assert p["parts"].tolist() == [[1, 0], [3, 0], [2, 0], [4, 0], [0, 0]]
+    p = np_plan(build_cascade_plan(bt, ctx, 16, 32, 8, chunk_tokens=16, part_tokens=16))
     assert p["tiles"].tolist() == [[0, 3, 0, 16], [0, 3, 16, 32]] and p["max_chunks"] == 2
-    with pytest.raises(ValueError):
-        build_cascade_plan(bt, ctx, 16, 32, 8, chunk_tokens=24)
+    # 16-token partitions: lengths 8 | 16 16 | 16 2 | 16 4 | 10
+    assert p["max_parts"] == 2
+    assert p["parts"].tolist() == [[1, 0], [1, 1], [2, 0], [3, 0], [4, 0], [0, 0], [3, 1], [2, 1]]
+    for bad in (dict(chunk_tokens=24), dict(part_tokens=24), dict(part_tokens=2048), dict(part_tokens=0)):
+        with pytest.raises(ValueError):
+            build_cascade_plan(bt, ctx, 16, 32, 8, **bad)
     with pytest.raises(ValueError):
         build_cascade_plan(bt, ctx, 16, 30, 8)
+
+
+def test_tail_partitions_known_answers():
+    assert tail_partitions(np.array([0, 5, 64, 65]), 32).tolist() == \
+        [[2, 0], [2, 1], [3, 0], [3, 1], [1, 0], [3, 2], [0, 0]]
+    assert tail_partitions(np.array([], dtype=np.int64), 16).shape == (0, 2)
+    assert tail_partitions(np.array([-3]), 16).tolist() == [[0, 0]]
 
 
 def test_chunk_fills_the_cus():
@@ -124,9 +138,18 @@ def test_plan_invariants(seed):
     p = np_plan(build_cascade_plan(bt, ctx, bs, Hq, Hkv, num_cus=64))
     group = Hq // Hkv
     B = bt.shape[0]
-    assert sorted(p["order"].tolist()) == list(range(B))
     tail = ctx - p["prefix_lens"]
-    assert (np.diff(tail[p["order"]]) <= 0).all() and p["max_tail"] == tail.max()
+    P = p["part_tokens"]
+    assert P % 16 == 0 and P % bs == 0
+    seen = {}
+    lengths = []
+    for s_, k in p["parts"].tolist():
+        seen.setdefault(s_, []).append(k)
+        lengths.append(min(P, tail[s_] - k * P))
+    for s_ in range(B):
+        n = max(1, -(-int(tail[s_]) // P))
+        assert sorted(seen[s_]) == list(range(n)) and n <= p["max_parts"]
+    assert (np.diff(lengths) <= 0).all()
     assert p["chunk"] % 16 == 0 and p["chunk"] % bs == 0
     covered = {}
     for mb, mc, t0, t1 in p["tiles"].tolist():
@@ -171,15 +194,21 @@ def cascade_restated(q, kc, vc, bt, ctx, Hkv, scale, bs, max_seq_len, plan, alib
             bias = None if alibi is None else orc.alibi_bias(alibi, c)
             parts[s].append(orc.partition_stats(q[s], k, v, scale, bias, t0, hi))
     out = np.zeros_like(q)
-    for s in range(B):
+    for s, kp in plan["parts"].tolist():
         c = int(ctx[s])
         if c == 0 or c > max_seq_len:
             continue
         P = min(int(plan["prefix_lens"][s]), c)
-        if P < c:
+        lo = P + kp * plan["part_tokens"]
+        hi = min(c, lo + plan["part_tokens"])
+        if lo < hi:
             k, v = orc.gather_kv(kc, vc, bt[s], c)
             bias = None if alibi is None else orc.alibi_bias(alibi, c)
-            parts[s].append(orc.partition_stats(q[s], k, v, scale, bias, P, c))
+            parts[s].append(orc.partition_stats(q[s], k, v, scale, bias, lo, hi))
+    for s in range(B):
+        c = int(ctx[s])
+        if c == 0 or c > max_seq_len:
+            continue
         ps = parts[s]
         out[s] = orc.lse_merge(np.stack([x[0] for x in ps]), np.stack([x[1] for x in ps]),
                                np.stack([x[2] for x in ps]))
@@ -197,11 +226,14 @@ def restated_case(seed, bs=16, Hq=8, Hkv=2, D=32, alibi=False):
     return q, kc, vc, bt, ctx, Hkv, 1 / np.sqrt(D), bs, bt.shape[1] * bs, slopes
 
 
-@pytest.mark.parametrize("seed,bs,alibi,chunk", [(1, 16, False, None), (2, 8, True, 16), (3, 32, False, 32)])
-def test_plan_restated_equals_single_softmax(seed, bs, alibi, chunk):
+@pytest.mark.parametrize("seed,bs,alibi,chunk,part", [(1, 16, False, None, None), (2, 8, True, 16, 16),
+                                                     (3, 32, False, 32, 32)])
+def test_plan_restated_equals_single_softmax(seed, bs, alibi, chunk, part):
     q, kc, vc, bt, ctx, Hkv, scale, bs, msl, slopes = restated_case(seed, bs=bs, alibi=alibi)
     ctx[3] = 0
-    plan = np_plan(build_cascade_plan(bt, ctx, bs, q.shape[1], Hkv, chunk_tokens=chunk))
+    plan = np_plan(build_cascade_plan(bt, ctx, bs, q.shape[1], Hkv, chunk_tokens=chunk, part_tokens=part))
+    if part is not None:
+        assert plan["max_parts"] > 1
     assert plan["tiles"].shape[0] > 0
     got = cascade_restated(q, kc, vc, bt, ctx, Hkv, scale, bs, msl, plan, slopes)
     exp = orc.paged_attention(q.astype(np.float32), kc.astype(np.float32), vc.astype(np.float32), bt, ctx, Hkv,
@@ -230,4 +262,13 @@ def test_planted_plan_mistakes_are_caught():
     t = bad["tiles"][0].copy()
     bad["tiles"][0] = (t[0] + 1, t[1] - 1, t[2], t[3])
     s = int(plan["members"][t[0]])
+    assert not np.allclose(cascade_restated(q, kc, vc, bt, ctx, Hkv, scale, bs, msl, bad)[s], exp[s], atol=1e-6)
+    # a tail partition left out: its tokens are never counted
+    plan = np_plan(build_cascade_plan(bt, ctx, bs, q.shape[1], Hkv, part_tokens=16))
+    np.testing.assert_allclose(cascade_restated(q, kc, vc, bt, ctx, Hkv, scale, bs, msl, plan), exp,
+                               atol=1e-12, rtol=1e-10)
+    bad = dict(plan)
+    s, k = plan["parts"][0]
+    assert k >= 0 and (plan["parts"][:, 0] == s).sum() > 1
+    bad["parts"] = plan["parts"][1:]
     assert not np.allclose(cascade_restated(q, kc, vc, bt, ctx, Hkv, scale, bs, msl, bad)[s], exp[s], atol=1e-6)

@@ -3,15 +3,17 @@ against the oracle and against paged_attention_v1 on the same inputs.
 
 The plan comes from the host's block tables (build_cascade_plan): a prefix
 pass attends every member's query rows to each group's shared blocks, a tail
-pass streams each sequence's remaining tokens and folds the prefix partials
-in.  Cases: one group of 256 (the radix-shared shape), several groups with
-different prefixes plus unshared sequences, prefixes split into many chunks
-(more than four per row: the tail folds them four at a time), empty and
-over-long contexts, block ids outside the pool inside a shared prefix,
-ALiBi, block sizes 8/16/32, head sizes 64/128, GQA 1/2/4/7/8, float16 and
-bfloat16 queries, FP8 E4M3 caches with k_scale / v_scale, shapes the cascade
-kernels leave to the one-pass decode (float32 query, head size 96, tails past
-2048 tokens), and repeated calls (bit-identical)."""
+pass streams each sequence's remaining tokens in partitions, and a merge
+folds the partial states.  Cases: one group of 256 (the radix-shared shape),
+several groups with different prefixes plus unshared sequences, prefixes
+split into many chunks (more than four per row: the merge folds them four at
+a time), tails in many partitions (16-token partitions, 2600-token tails)
+and in one (1024-token partitions), sequences without a prefix over several
+partitions, empty and over-long contexts, block ids outside the pool inside
+a shared prefix, ALiBi, block sizes 8/16/32, head sizes 64/128, GQA
+1/2/4/7/8, float16 and bfloat16 queries, FP8 E4M3 caches with k_scale /
+v_scale, shapes the cascade kernels leave to the one-pass decode (float32
+query, head size 96), and repeated calls (bit-identical)."""
 
 import math
 
@@ -157,7 +159,7 @@ def test_fp8_query_types_head_sizes(q_dtype, D):
     check(c, fp8=True)
 
 
-@pytest.mark.parametrize("q_dtype,D,tail", [("float32", 128, 300), ("bfloat16", 96, 300), ("bfloat16", 128, 2600)])
+@pytest.mark.parametrize("q_dtype,D,tail", [("float32", 128, 300), ("bfloat16", 96, 300)])
 def test_shapes_left_to_the_one_pass_decode(q_dtype, D, tail):
     c = radix_case(7900 + D, B=64, Hq=32, Hkv=8, D=D, bs=16, prefix_tokens=256, suffix_lo=tail - 100,
                    suffix_hi=tail, dtype="bfloat16", q_dtype=q_dtype)
@@ -168,10 +170,26 @@ def test_shapes_left_to_the_one_pass_decode(q_dtype, D, tail):
     np.testing.assert_array_equal(got, to_f64(ref))  # the same kernels ran
 
 
-def test_no_groups_is_plain_tail_decode():
+@pytest.mark.parametrize("part", [None, 16, 1024])
+def test_long_tails_in_partitions(part):
+    c = radix_case(7950, B=64, Hq=32, Hkv=8, D=128, bs=16, prefix_tokens=256, suffix_lo=2500, suffix_hi=2600)
+    plan, _ = check(c, part_tokens=part)
+    assert plan.max_parts == -(-int((c["ctx"] - 256).max()) // plan.part_tokens)
+
+
+@pytest.mark.parametrize("part", [None, 32])
+def test_no_groups_is_plain_tail_decode(part):
+    # no prefix anywhere: rows of one partition are written by the tail
+    # pass, longer ones by the merge
     c = groups_case(8000, [], unshared=300, suffix=(1, 700))
-    plan, _ = check(c)
-    assert plan.tiles.shape[0] == 0
+    plan, _ = check(c, part_tokens=part)
+    assert plan.tiles.shape[0] == 0 and plan.max_parts > 1
+
+
+def test_very_short_tails():
+    # tails of 1-8 tokens behind a 2048-token prefix
+    c = radix_case(8050, B=128, Hq=32, Hkv=8, D=128, bs=16, prefix_tokens=2048, suffix_lo=1, suffix_hi=8)
+    check(c)
 
 
 def test_repeat_calls_are_bit_identical():
