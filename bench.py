@@ -35,11 +35,16 @@ Printed: ONE JSON line with the driver's fields plus
                 [rows, Hkv, D] buffer through slot tables (block size 1) and
                 the flash layout [blocks, 16, Hkv, D];
   fp8_kv        the decode layer over FP8 E4M3 caches (half the KV bytes);
+  batch_sweep   the decode layer at batch 8 .. 128;
+  ref_decode_b1 the reference's own decode benchmark (batch 1, fp16, seq
+                1024 / 4096 / 8192), with its CPU gather + SDPA beside it;
+  ref_append    the reference's own append benchmark (fp16, N = 1 .. 1024
+                tokens), with a CPU scatter beside it;
   cpu_baseline  the reference's gather + SDPA decode restated in torch on
                 this host's cores, on the same inputs (full batch, one layer).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-append] [--no-splitk] [--no-radix]
-                       [--no-rows] [--no-fp8] [--only LEG]
+                       [--no-rows] [--no-fp8] [--no-sweep] [--no-ref] [--only LEG]
 """
 
 from __future__ import annotations
@@ -79,10 +84,13 @@ def parse_args():
     ap.add_argument("--no-rows", action="store_true", help="skip the token-row (MHATokenPool) decode measurement")
     ap.add_argument("--no-fp8", action="store_true", help="skip the FP8-cache decode measurement")
     ap.add_argument("--no-sweep", action="store_true", help="skip the batch-size sweep of the decode layer")
+    ap.add_argument("--no-ref", action="store_true",
+                    help="skip the reference's own benchmark configurations (B1 fp16 decode, fp16 append counts)")
     ap.add_argument("--lib", help="load libpagedkv_gfx950.so from this path instead of the package's (a build of the "
                                   "same sources with other compile-time settings, e.g. make EXTRA_HIPFLAGS=... "
                                   "OUTDIR=...), for A/B profiles")
-    ap.add_argument("--only", choices=["decode", "append", "copy", "splitk", "radix", "radix_fp8", "rows", "fp8", "sweep"],
+    ap.add_argument("--only", choices=["decode", "append", "copy", "splitk", "radix", "radix_fp8", "rows", "fp8", "sweep",
+                                       "ref_decode", "ref_append"],
                     help="run one leg and print its own short JSON line (for counter collection under "
                          "rocprofv3 --pmc): the decode layer, the token-major append, or a plain 1 GiB device "
                          "copy whose FETCH_SIZE / WRITE_SIZE calibrate the counters")
@@ -527,6 +535,135 @@ def bench_radix(dev, kernels, steps: int = 40, warmup: int = 5, layers: int = 4,
                         f"cascade and v1 timed alternately on the same steps"))
 
 
+def bench_ref_decode(dev, kernels, seq_lens=(1024, 4096, 8192), cpu_budget_s: float = 1.0):
+    """The reference's own decode benchmark configuration
+    (tests/bench_paged_vs_gather.py:9-45,120-123): batch 1, float16, 32 query
+    / 8 KV heads, D 128, block_size 16, a pool of seq/16 + 10 blocks, the
+    block table 0 .. seq/16 - 1, caches filled through reshape_and_cache
+    with slots 0 .. seq-1 from uniform [0, 1) keys and values, a uniform
+    query; seq in {1024, 4096, 8192}.  Per seq: paged_attention_v1's device
+    time per call as a HIP graph of back-to-back calls on the one cache (as
+    the reference reuses it: L2 and the Infinity Cache hold it) and on
+    caches rotated past the Infinity Cache (HBM-bound, the % of 8 TB/s
+    quoted), and the CPU baseline: the reference's gather + SDPA on the same
+    inputs, torch on this host's cores."""
+    from oracle import cpu_baseline as cb
+
+    Hq, Hkv, D, bs, x = 32, 8, 128, 16, 8
+    scale = 1.0 / math.sqrt(D)
+    g = torch.Generator(device=dev)
+    g.manual_seed(1006)
+    rows = []
+    for seq in seq_lens:
+        nb = -(-seq // bs) + 10
+        pool_bytes = nb * bs * Hkv * D * 2 * 2
+        npools = max(2, -(-700_000_000 // pool_bytes))
+        q = torch.rand((1, Hq, D), generator=g, device=dev).to(torch.float16)
+        slots = torch.arange(seq, dtype=torch.int32, device=dev)
+        pools = []
+        for i in range(npools):
+            kc = torch.zeros((nb, Hkv, D // x, bs, x), dtype=torch.float16, device=dev)
+            vc = torch.zeros((nb, Hkv, D, bs), dtype=torch.float16, device=dev)
+            ks = torch.rand((seq, Hkv, D), generator=g, device=dev).to(torch.float16)
+            vs = torch.rand((seq, Hkv, D), generator=g, device=dev).to(torch.float16)
+            kernels.reshape_and_cache(ks, vs, kc, vc, slots)
+            pools.append((kc, vc))
+        bt = torch.arange(seq // bs, dtype=torch.int32, device=dev).reshape(1, -1)
+        ctx = torch.tensor([seq], dtype=torch.int32, device=dev)
+        nbytes = decode_bytes(np.array([seq]), 1, Hq, Hkv, D, bs)
+
+        def call(i, rotate):
+            kc, vc = pools[i % npools] if rotate else pools[0]
+            return kernels.paged_attention_v1(q, kc, vc, bt, ctx, Hkv, scale, bs, seq)
+
+        hot = graph_launch_ms(lambda i: call(i, False), 100)
+        cold = graph_launch_ms(lambda i: call(i, True), npools)
+        gbs = nbytes / (cold * 1e-3) / 1e9
+        kc0, vc0 = pools[0]
+        qc, k5, v5, btc, ctxc = q.cpu(), kc0.cpu(), vc0.cpu(), bt.cpu(), ctx.cpu()
+        t = cb.time_decode(qc, k5, v5, btc, ctxc, bs, scale, budget_s=cpu_budget_s,
+                           fn=cb.gather_sdpa_decode_paged5d)
+        ref = cb.gather_sdpa_decode_paged5d(qc, k5, v5, btc, ctxc, bs, scale)
+        diff = (call(0, False).float().cpu() - ref.float()).abs().max().item()
+        rows.append(dict(seq_len=seq, bytes_per_call=nbytes, us_same_cache=round(hot * 1e3, 2),
+                         us=round(cold * 1e3, 2), gbs=round(gbs, 1), frac=round(gbs / PEAK_GBS, 4),
+                         caches_rotated=npools,
+                         cpu_baseline=dict(us=round(t["median_s"] * 1e6, 1),
+                                           gbs=round(nbytes / t["median_s"] / 1e9, 2), cores=t["threads"],
+                                           kind="port", iters=t["iters"]),
+                         max_abs_diff_vs_cpu=round(diff, 5)))
+        del pools
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+    return dict(workload="reference decode benchmark: B1, fp16, 32 q / 8 kv heads, D128, bs16, contiguous "
+                         "blocks, seq in {1024, 4096, 8192}", rows=rows,
+                method="HIP graph of back-to-back calls (median of 5 replays): us_same_cache on one cache, us "
+                       "over caches rotated past 700 MB; CPU: gather + SDPA (relayout included), torch CPU, "
+                       "median over a 1 s sample")
+
+
+def bench_ref_append(dev, kernels, counts=(1, 8, 16, 64, 128, 256, 512, 1024), cpu_budget_s: float = 0.5):
+    """The reference's own append benchmark configuration
+    (tests/bench_reshape_and_cache.py:29-37,60-89): float16, 8 KV heads,
+    D 128, block_size 16, a pool of ceil(N/16) + 1 blocks, slots 0 .. N-1,
+    uniform [0, 1) keys and values, N in {1, 8, 16, 64, 128, 256, 512,
+    1024}.  Per N: device time per launch as a HIP graph of 100 launches,
+    the host-synchronous call latency the reference measures (call then
+    synchronise, median of 100 after 20 warm-ups), % of 8 TB/s on the
+    algorithmic bytes (K and V read and written, the slot ids read), the
+    reference's own write bandwidth (K and V bytes written / device time),
+    and the CPU baseline: the same scatter with torch on this host's
+    cores."""
+    from oracle import cpu_baseline as cb
+
+    H, D, bs, x = 8, 128, 16, 8
+    g = torch.Generator(device=dev)
+    g.manual_seed(1007)
+    rows = []
+    for n in counts:
+        nb = -(-n // bs) + 1
+        kc = torch.zeros((nb, H, D // x, bs, x), dtype=torch.float16, device=dev)
+        vc = torch.zeros((nb, H, D, bs), dtype=torch.float16, device=dev)
+        k = torch.rand((n, H, D), generator=g, device=dev).to(torch.float16)
+        v = torch.rand((n, H, D), generator=g, device=dev).to(torch.float16)
+        slots = torch.arange(n, dtype=torch.int32, device=dev)
+
+        def call(i):
+            kernels.reshape_and_cache(k, v, kc, vc, slots)
+
+        dev_ms = graph_launch_ms(call, 100)
+        for _ in range(20):
+            call(0)
+        torch.cuda.synchronize()
+        lat = []
+        for _ in range(100):
+            t0 = time.perf_counter()
+            call(0)
+            torch.cuda.synchronize()
+            lat.append(time.perf_counter() - t0)
+        lat.sort()
+        written = n * H * D * 2 * 2
+        nbytes = 2 * written + n * 4
+        kcc, vcc = kc.cpu().zero_(), vc.cpu().zero_()
+        kk, vv, ss = k.cpu(), v.cpu(), slots.cpu()
+        t = cb.time_calls(lambda: cb.scatter_append_paged5d(kk, vv, kcc, vcc, ss), budget_s=cpu_budget_s)
+        same = bool(torch.equal(kcc, kc.cpu()) and torch.equal(vcc, vc.cpu()))
+        rows.append(dict(tokens=n, bytes_per_launch=nbytes, us=round(dev_ms * 1e3, 3),
+                         gbs=round(nbytes / (dev_ms * 1e-3) / 1e9, 1),
+                         frac=round(nbytes / (dev_ms * 1e-3) / 1e9 / PEAK_GBS, 4),
+                         write_gbs=round(written / (dev_ms * 1e-3) / 1e9, 1),
+                         call_latency_us=round(lat[len(lat) // 2] * 1e6, 1),
+                         cpu_baseline=dict(us=round(t["median_s"] * 1e6, 2),
+                                           gbs=round(nbytes / t["median_s"] / 1e9, 2), cores=t["threads"],
+                                           kind="port", iters=t["iters"]),
+                         cpu_equal=same))
+    return dict(workload="reference append benchmark: fp16, 8 kv heads, D128, bs16, slots 0..N-1, "
+                         "N in {1, 8, 16, 64, 128, 256, 512, 1024}", rows=rows,
+                method="device: HIP graph of 100 launches (median of 5 replays); call_latency: call + "
+                       "synchronise, median of 100; CPU: torch scatter into the paged 5-D caches, median over "
+                       "a 0.5 s sample")
+
+
 def bench_cpu(res, budget_s):
     """CPU baseline leg: the oracle package's torch-CPU gather + SDPA, same
     inputs (layer 0), full batch.  The reported value follows
@@ -579,6 +716,10 @@ def only_leg(args, dev, kernels):
         print(json.dumps(dict(leg="fp8", **bench_fp8(dev, kernels))))
     elif args.only == "sweep":
         print(json.dumps(dict(leg="sweep", **bench_batch_sweep(dev, kernels))))
+    elif args.only == "ref_decode":
+        print(json.dumps(dict(leg="ref_decode", **bench_ref_decode(dev, kernels))))
+    elif args.only == "ref_append":
+        print(json.dumps(dict(leg="ref_append", **bench_ref_append(dev, kernels))))
     else:
         n = 1 << 30
         src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
@@ -679,6 +820,9 @@ def main():
         line["fp8_kv"] = bench_fp8(dev, kernels)
     if not args.no_sweep:
         line["batch_sweep"] = bench_batch_sweep(dev, kernels)
+    if not args.no_ref:
+        line["ref_decode_b1"] = bench_ref_decode(dev, kernels)
+        line["ref_append"] = bench_ref_append(dev, kernels)
     if not args.no_cpu:
         line["cpu_baseline"] = bench_cpu(res, args.cpu_budget)
     else:

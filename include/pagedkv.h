@@ -104,14 +104,19 @@ int pkv_reshape_and_cache(const void* key, const void* value,
                           void* stream);
 
 /*
- * Workspace bytes that pkv_paged_attention needs for these sizes
- * (per-partition (max, sum) pairs and per-partition outputs, float32).
- * partition_size = 0 selects the single-pass (v1) semantics; the library
- * then chooses its own schedule.  The workspace needs no initialisation and
- * each launch reads only what it wrote, so calls ordered on one stream may
- * share one buffer; calls that overlap in time must not.  Returns 0 for
- * invalid sizes.
+ * Workspace bytes that pkv_paged_attention needs for these sizes:
+ * PKV_COUNTER_BYTES of arrival counters, then per-partition (max, sum)
+ * pairs and per-partition outputs (float32).  partition_size = 0 selects
+ * the single-pass (v1) semantics; the library then chooses its own
+ * schedule.  Zero-fill a workspace once, when it is allocated: its first
+ * PKV_COUNTER_BYTES count the partitions of each (sequence, KV head) as
+ * their workgroups finish, and every call leaves them zero again; the rest
+ * needs no initialisation (each launch reads only what it wrote).  Calls
+ * ordered on one stream may share one workspace, also with
+ * pkv_paged_attention_cascade; calls that overlap in time must not.
+ * Returns 0 for invalid sizes.
  */
+#define PKV_COUNTER_BYTES 65536
 size_t pkv_paged_attention_workspace_size(int32_t num_seqs, int32_t num_heads,
                                           int32_t num_kv_heads,
                                           int32_t head_size,
@@ -142,8 +147,12 @@ size_t pkv_paged_attention_workspace_size(int32_t num_seqs, int32_t num_heads,
  * most 4 and contexts of at most 8192 tokens -- 4096 over FP8 caches at
  * head sizes 64 and 128 -- items of four sequences that share the MFMA
  * columns, so that tiles the four map to the same block are read once);
- * otherwise a partition kernel, plus a log-sum-exp merge kernel when a
- * sequence has more than one partition.
+ * otherwise a partition kernel.  When a sequence has more than one
+ * partition: with at most 8 partitions per sequence (paged layout, and
+ * num_seqs * num_kv_heads counters within the counter region), the
+ * workgroup that finishes a sequence's last partition merges them (log-sum-
+ * exp, in partition order: results do not depend on which workgroup
+ * merges); otherwise a log-sum-exp merge kernel follows.
  * query   : [num_seqs, num_heads, head_size], row stride q_stride.
  * out     : [num_seqs, num_heads, head_size] contiguous, same dtype as
  *           query, 16-byte aligned.
@@ -247,9 +256,11 @@ typedef struct pkv_cascade_plan {
 /*
  * Workspace bytes of pkv_paged_attention_cascade: the larger of the one-pass
  * decode's (pkv_paged_attention_workspace_size with partition_size 0) and
- * the partial states' (num_seqs * num_heads * (max_chunks + max_parts) *
- * (head_size + 2) float32, in four parts each 256-byte aligned).  Returns 0
- * for invalid sizes.
+ * the counter region plus the partial states' (num_seqs * num_heads *
+ * (max_chunks + max_parts) * (head_size + 2) float32, in four parts each
+ * 256-byte aligned).  Zero-filled once when allocated, as for
+ * pkv_paged_attention (the cascade leaves the counter region untouched).
+ * Returns 0 for invalid sizes.
  */
 size_t pkv_paged_attention_cascade_workspace_size(int32_t num_seqs,
                                                   int32_t num_heads,
@@ -310,9 +321,11 @@ int pkv_paged_attention_cascade(void* out, const void* query,
  * PKV_NOALLOC_SCRATCH_BYTES per GPU, which the library holds from its first
  * call on that GPU until the process ends; a call whose sizes need more
  * (pkv_paged_attention_workspace_size) fails with PKV_ERR_UNSUPPORTED
- * before any HIP call.  The kernels need no initialised scratch and read
- * only what the same call wrote, so stale contents from an earlier call do
- * not matter.  Every call on one GPU shares that GPU's array: calls that
+ * before any HIP call, whether or not the launch would use it.  The array
+ * is laid out as a workspace and starts zeroed, so its counter region is
+ * zero as pkv_paged_attention requires (every call leaves it zero); the rest
+ * is read only where the same call wrote it, so stale contents from an
+ * earlier call do not matter.  Every call on one GPU shares that GPU's array: calls that
  * overlap in time on one GPU (different streams, or threads) race and give
  * undefined results; order them on one stream.  The first call on a GPU
  * looks the array's address up with hipGetSymbolAddress (no allocation).

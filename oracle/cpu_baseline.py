@@ -27,6 +27,11 @@ first relays the paged 5-D caches out as token-major [nb * bs, Hkv, D]
 gather_sdpa_decode_paged5d does the same, so that the relayout is inside
 whatever is timed.
 
+scatter_append_paged5d is the append (reshape_and_cache) restated the same
+way: each token's K and V rows written in place into the paged 5-D caches
+at block slot // bs, offset slot % bs, slots < 0 skipped
+(reshape_and_cache.metal:35-69), with torch indexing on the host.
+
 The 1e-6 in the reference kernel's softmax denominator is a kernel detail
 (paged_attention_kernels.metal:144), absent from SDPA, so results differ
 from the oracle by a relative 1e-6 plus SDPA's own rounding.
@@ -109,6 +114,44 @@ def gather_sdpa_decode_paged5d(q, key_cache, value_cache, block_tables, context_
     first, as the reference's benchmark does, then gather + SDPA."""
     k_pool, v_pool = paged5d_to_token_major(key_cache, value_cache)
     return gather_sdpa_decode(q, k_pool, v_pool, block_tables, context_lens, block_size, scale, seqs)
+
+
+def scatter_append_paged5d(key: torch.Tensor, value: torch.Tensor, key_cache: torch.Tensor,
+                           value_cache: torch.Tensor, slot_mapping: torch.Tensor) -> None:
+    """In place: key / value [N, H, D] into key_cache [nb, H, D/x, bs, x] and
+    value_cache [nb, H, D, bs] (same dtype), token i at slot_mapping[i]."""
+    nb, H, dx, bs, x = key_cache.shape
+    slots = slot_mapping.to(torch.int64)
+    keep = slots >= 0
+    s = slots[keep]
+    blk, off = s // bs, s % bs
+    k = key[keep].reshape(-1, H, dx, x)
+    v = value[keep]
+    key_cache.permute(0, 3, 1, 2, 4)[blk, off] = k      # [n, H, D/x, x] at (block, offset)
+    value_cache.permute(0, 3, 1, 2)[blk, off] = v       # [n, H, D] at (block, offset)
+
+
+def time_calls(fn, budget_s: float = 1.0, min_iters: int = 5) -> dict:
+    """Median wall time of fn() over >= min_iters runs (after one warm-up),
+    stopping once ``budget_s`` of timed work is done, on host_threads()
+    threads."""
+    threads = host_threads()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        fn()
+        times = []
+        t_all = time.perf_counter()
+        while len(times) < min_iters or time.perf_counter() - t_all < budget_s:
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+            if len(times) >= 10000:
+                break
+        times.sort()
+        return dict(median_s=times[len(times) // 2], iters=len(times), threads=threads, cpu=cpu_model())
+    finally:
+        torch.set_num_threads(prev)
 
 
 def time_decode(q, k_pool, v_pool, block_tables, context_lens, block_size, scale,

@@ -1523,6 +1523,100 @@ __device__ __forceinline__ void unit_heads(const DecodeParams& p, int unit, int&
 }
 
 // ---------------------------------------------------------------------------
+// The partition kernel's own merge.  Partition states cross workgroups inside
+// one launch: each workgroup stores its state, then counts it on its
+// (sequence, unit)'s arrival counter, and the workgroup whose state is the
+// last to arrive merges.  gfx950's L2 caches are per XCD and not coherent
+// with one another for ordinary accesses, so the states are written and read
+// with agent-scope relaxed atomic accesses, which gfx950 issues as ordinary
+// vector loads and stores carrying the SC1 cache-policy bit: each one is
+// coherent at agent scope by itself, with no cache-wide write-back or
+// invalidate.  A writer waits until its stores have completed (s_waitcnt
+// vmcnt(0)) before its relaxed agent-scope atomic add on the counter, so a
+// workgroup that sees the last count can only load states that are already
+// at the coherence point.  The last arrival sets the counter back to zero
+// for the next launch.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void store_agent2(float* p, float a, float b) {
+  const uint64_t v = (uint64_t)__float_as_uint(a) | ((uint64_t)__float_as_uint(b) << 32);
+  __hip_atomic_store(reinterpret_cast<uint64_t*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float2 load_agent2(const float* p) {
+  const uint64_t v =
+      __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return make_float2(__uint_as_float((uint32_t)v), __uint_as_float((uint32_t)(v >> 32)));
+}
+// Waits until this wavefront's vector memory accesses so far have completed;
+// the compiler fences keep every access on its side of the wait.
+__device__ __forceinline__ void wait_stores() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0); expcnt and lgkmcnt left at their maxima
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+// Counts one arrival; true for the expected-th, which resets the counter
+// (every arrival of this launch has happened by then).
+__device__ __forceinline__ bool arrive_last(int32_t* counter, int expected) {
+  const bool last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == expected - 1;
+  if (last) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return last;
+}
+
+// Log-sum-exp merge of the `count` partition states (slots 0 .. count-1)
+// of the nh rows row0 .. row0 + nh - 1, by the whole workgroup, and the rows
+// written: thread t takes 4 dimensions (chunk t % (D/4)) of one row per
+// pass and folds the states in slot order, so the result does not depend on
+// which workgroup merges.  The weights are those of the merge kernel
+// (paged_decode_reduce_kernel): sum * exp2(max - running max) per state,
+// states whose max is -inf skipped; out = weighted sum / (weight sum +
+// 1e-6).
+template <class QT, int D, int NT>
+__device__ __forceinline__ void merge_part_states(const DecodeParams& p, int64_t row0, int nh, int count) {
+  using QS = typename Elem<QT>::storage;
+  static_assert(D % 4 == 0, "head sizes are multiples of 8");
+  constexpr int CH = D / 4;
+  constexpr int RPP = NT / CH;  // rows per pass
+  constexpr int U = kMergeGroup;
+  const int t = threadIdx.x;
+  const int c = t % CH, hr = t / CH;
+  for (int hb = 0; hb < nh; hb += RPP) {
+    const bool act = hr < RPP && hb + hr < nh;
+    const int64_t row = row0 + (act ? hb + hr : 0);
+    float m = -INFINITY, l = 0.f;
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+    float2 e[U];
+    float4 o[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      e[u] = make_float2(-INFINITY, 0.f);
+      o[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (act && u < count) {
+        const int64_t slot = row * p.max_parts + u;
+        e[u] = load_agent2(p.ws_ml + slot * 2);
+        const float2 lo = load_agent2(p.ws_o + slot * D + 4 * c);
+        const float2 hi = load_agent2(p.ws_o + slot * D + 4 * c + 2);
+        o[u] = make_float4(lo.x, lo.y, hi.x, hi.y);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) m = fmaxf(m, e[u].x);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const bool use = e[u].x != -INFINITY;
+      const float w = use ? e[u].y * exp2f(e[u].x - m) : 0.f;
+      l += w;
+      a.x += use ? w * o[u].x : 0.f;
+      a.y += use ? w * o[u].y : 0.f;
+      a.z += use ? w * o[u].z : 0.f;
+      a.w += use ? w * o[u].w : 0.f;
+    }
+    if (act) {
+      const float inv = 1.f / (l + 1e-6f);
+      store4<QT>(static_cast<QS*>(p.out) + row * D + 4 * c, a.x * inv, a.y * inv, a.z * inv, a.w * inv);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Partition kernel: one workgroup of NW wavefronts per (partition, sequence,
 // unit).
 // ---------------------------------------------------------------------------
@@ -1583,23 +1677,44 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_part_kernel(DecodeParams
 
   float M, L;
   merge_waves<D, NW>(acc, s_red, s_m, s_l, wave, lane, g, col, M, L);
-  if (wave != 0 || col >= nh) return;
   const int64_t hrow = (int64_t)seq * p.num_heads + h0 + col;
   if (nparts == 1) {
-    write_output<QT, D>(p, hrow, acc, L, g);
+    if (wave == 0 && col < nh) write_output<QT, D>(p, hrow, acc, L, g);
     return;
   }
-  const int64_t slot = hrow * p.max_parts + part;
-  const float invl = L > 0.f ? p.v_scale / L : 0.f;
-  float* wo = p.ws_o + slot * D;
+  const bool fused = p.counters != nullptr;
+  if (wave == 0 && col < nh) {
+    const int64_t slot = hrow * p.max_parts + part;
+    const float invl = L > 0.f ? p.v_scale / L : 0.f;
+    float* wo = p.ws_o + slot * D;
 #pragma unroll
-  for (int dt = 0; dt < DT; ++dt) {
-    const int d = 16 * dt + 4 * g;
-    if (D % 16 == 0 || d < D)
-      *reinterpret_cast<float4*>(wo + d) =
-          make_float4(acc.o[dt][0] * invl, acc.o[dt][1] * invl, acc.o[dt][2] * invl, acc.o[dt][3] * invl);
+    for (int dt = 0; dt < DT; ++dt) {
+      const int d = 16 * dt + 4 * g;
+      if (D % 16 != 0 && d >= D) continue;
+      const float x0 = acc.o[dt][0] * invl, x1 = acc.o[dt][1] * invl;
+      const float x2 = acc.o[dt][2] * invl, x3 = acc.o[dt][3] * invl;
+      if (fused) {
+        store_agent2(wo + d, x0, x1);
+        store_agent2(wo + d + 2, x2, x3);
+      } else {
+        *reinterpret_cast<float4*>(wo + d) = make_float4(x0, x1, x2, x3);
+      }
+    }
+    if (g == 0) {
+      if (fused)
+        store_agent2(p.ws_ml + slot * 2, M, L);
+      else
+        *reinterpret_cast<float2*>(p.ws_ml + slot * 2) = make_float2(M, L);
+    }
   }
-  if (g == 0) *reinterpret_cast<float2*>(p.ws_ml + slot * 2) = make_float2(M, L);
+  if (!fused) return;  // the merge kernel follows
+
+  // Arrival: the workgroup whose state is the row's last merges them all.
+  __shared__ int s_last;
+  if (wave == 0) wait_stores();
+  if (tid == 0) s_last = arrive_last(p.counters + (int64_t)seq * p.units + unit, nparts);
+  __syncthreads();
+  if (s_last) merge_part_states<QT, D, 64 * NW>(p, (int64_t)seq * p.num_heads + h0, nh, nparts);
 }
 
 // ---------------------------------------------------------------------------
@@ -2522,7 +2637,7 @@ static hipError_t launch_one(const DecodeParams& p, hipStream_t stream) {
   hipLaunchKernelGGL((paged_decode_part_kernel<QT, CT, D, BS, kPartWaves>), dim3((unsigned)nwg), dim3(64 * kPartWaves),
                      0, stream, p);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess || p.max_parts == 1) return e;
+  if (e != hipSuccess || p.max_parts == 1 || p.counters != nullptr) return e;
   const int64_t rows = (int64_t)p.num_seqs * p.num_heads;
   hipLaunchKernelGGL((paged_decode_reduce_kernel<QT, D>), dim3((unsigned)rows), dim3(64 * kMergeWaves), 0, stream, p);
   return hipGetLastError();

@@ -118,6 +118,8 @@ int resolve_partition(int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
 
 }  // namespace
 
+static_assert(PKV_COUNTER_BYTES == pkv::kCounterBytes, "the header's counter region is the kernels'");
+
 namespace pkv {
 DecodeWorkspace decode_workspace_layout(int32_t num_seqs, int32_t num_heads, int32_t head_size,
                                         int32_t max_parts) {
@@ -125,7 +127,7 @@ DecodeWorkspace decode_workspace_layout(int32_t num_seqs, int32_t num_heads, int
   auto align = [](size_t x) { return (x + 255) & ~size_t(255); };
   w.ml_bytes = align((size_t)num_seqs * num_heads * max_parts * 2 * sizeof(float));
   w.o_bytes = align((size_t)num_seqs * num_heads * max_parts * head_size * sizeof(float));
-  w.total = w.ml_bytes + w.o_bytes;
+  w.total = (size_t)kCounterBytes + w.ml_bytes + w.o_bytes;
   return w;
 }
 CascadeWorkspace cascade_workspace_layout(int32_t num_seqs, int32_t num_heads, int32_t head_size,
@@ -136,7 +138,7 @@ CascadeWorkspace cascade_workspace_layout(int32_t num_seqs, int32_t num_heads, i
   w.o_bytes = align((size_t)num_seqs * num_heads * max_chunks * head_size * sizeof(float));
   w.tail_ml_bytes = align((size_t)num_seqs * num_heads * max_parts * 2 * sizeof(float));
   w.tail_o_bytes = align((size_t)num_seqs * num_heads * max_parts * head_size * sizeof(float));
-  w.total = w.ml_bytes + w.o_bytes + w.tail_ml_bytes + w.tail_o_bytes;
+  w.total = (size_t)kCounterBytes + w.ml_bytes + w.o_bytes + w.tail_ml_bytes + w.tail_o_bytes;
   return w;
 }
 }  // namespace pkv
@@ -388,8 +390,10 @@ int paged_attention_impl(void* out, const void* query, const void* key_cache, co
   p.block_tables = block_tables;
   p.context_lens = context_lens;
   p.alibi = alibi_slopes;
-  p.ws_ml = reinterpret_cast<float*>(ws);
-  p.ws_o = reinterpret_cast<float*>(ws + w.ml_bytes);
+  // The workspace starts with the partition kernel's arrival counters (zero
+  // between calls), then the partition states.
+  p.ws_ml = reinterpret_cast<float*>(ws + pkv::kCounterBytes);
+  p.ws_o = reinterpret_cast<float*>(ws + pkv::kCounterBytes + w.ml_bytes);
   p.num_blocks = num_blocks;
   p.q_stride = q_stride;
   p.k_block_stride = kbs;
@@ -412,6 +416,12 @@ int paged_attention_impl(void* out, const void* query, const void* key_cache, co
                  max_seq_len <= (rows ? pkv::persist_rows_max_seq(head_size) : pkv::kPersistMaxSeq);
   p.rows = rows;
   p.block_size = block_size;
+  // The paged layout's partition kernel merges its own partitions when a row
+  // has at most kMergeGroup of them and the batch's counters fit the counter
+  // region; otherwise (and for token rows) the merge kernel runs after it.
+  p.counters = (!rows && parts <= pkv::kMergeGroup && (int64_t)num_seqs * p.units * 4 <= pkv::kCounterBytes)
+                   ? reinterpret_cast<int32_t*>(ws)
+                   : nullptr;
   p.k_rows_bytes = p.v_rows_bytes = 0;
   if (rows) {
     const int64_t total_rows = num_blocks * block_size;
@@ -435,10 +445,11 @@ int paged_attention_impl(void* out, const void* query, const void* key_cache, co
     c.members = plan->members;
     c.tiles = reinterpret_cast<const int4*>(plan->tiles);
     c.parts = reinterpret_cast<const int2*>(plan->parts);
-    c.ws_ml = reinterpret_cast<float*>(ws);
-    c.ws_o = reinterpret_cast<float*>(ws + cw.ml_bytes);
-    c.ws_tail_ml = reinterpret_cast<float*>(ws + cw.ml_bytes + cw.o_bytes);
-    c.ws_tail_o = reinterpret_cast<float*>(ws + cw.ml_bytes + cw.o_bytes + cw.tail_ml_bytes);
+    char* cws = ws + pkv::kCounterBytes;
+    c.ws_ml = reinterpret_cast<float*>(cws);
+    c.ws_o = reinterpret_cast<float*>(cws + cw.ml_bytes);
+    c.ws_tail_ml = reinterpret_cast<float*>(cws + cw.ml_bytes + cw.o_bytes);
+    c.ws_tail_o = reinterpret_cast<float*>(cws + cw.ml_bytes + cw.o_bytes + cw.tail_ml_bytes);
     c.num_members = plan->num_members;
     c.num_tiles = plan->num_tiles;
     c.chunk = plan->chunk_tokens;

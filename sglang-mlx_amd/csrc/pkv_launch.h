@@ -98,7 +98,19 @@ struct DecodeParams {
   // Output scale: v_scale for FP8 caches (whose k_scale is folded into
   // scale_log2), 1 otherwise.
   float v_scale;
+  // Arrival counters of the partition kernel's own merge (null: the merge
+  // kernel runs after it): one per (sequence, unit), zero before a launch
+  // and left zero by it.
+  int32_t* counters;
 };
+
+// The partition kernel merges its own partitions (the workgroup whose state
+// arrives last folds them all) when a row has at most kMergeGroup of them;
+// deeper rows are merged by the merge kernel, whose many workgroups fetch
+// the states faster than one workgroup's dependent loads would.
+constexpr int kMergeGroup = 8;
+// Bytes at the start of every decode workspace that hold those counters.
+constexpr int64_t kCounterBytes = 65536;
 
 // Shared-prefix (cascade) decode plan, device arrays built on the host from
 // the block tables (see include/pagedkv.h, pkv_cascade_plan):

@@ -80,9 +80,11 @@ def _as_i32(t: torch.Tensor) -> torch.Tensor:
 
 
 # ---------------------------------------------------------------------------
-# Decode scratch, one buffer per (device, stream).  It needs no
-# initialisation and each launch reads only what it wrote, so calls ordered
-# on one stream share it whatever their shapes.
+# Decode scratch, one buffer per (device, stream).  Its first
+# PKV_COUNTER_BYTES are arrival counters that start at zero (a new buffer is
+# zero-filled) and that every call leaves at zero; the rest is read only
+# where the same launch wrote it.  So calls ordered on one stream share it
+# whatever their shapes.
 # ---------------------------------------------------------------------------
 _ws_lock = threading.Lock()
 _ws_cache: dict = {}
@@ -93,7 +95,7 @@ def _decode_scratch(dev: torch.device, stream: int, scratch_bytes: int) -> torch
     with _ws_lock:
         scratch = _ws_cache.get(key)
         if scratch is None or scratch.numel() < scratch_bytes:
-            scratch = torch.empty(max(scratch_bytes, 1 << 16), dtype=torch.uint8, device=dev)
+            scratch = torch.zeros(max(scratch_bytes, 1 << 17), dtype=torch.uint8, device=dev)
             _ws_cache[key] = scratch
         return scratch
 

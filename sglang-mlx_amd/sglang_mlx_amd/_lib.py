@@ -22,6 +22,7 @@ PKV_ERR_HIP = 3
 PKV_F32, PKV_F16, PKV_BF16, PKV_FP8_E4M3 = 0, 1, 2, 3
 PKV_LAYOUT_PAGED5D, PKV_LAYOUT_TOKEN_MAJOR = 0, 1
 PKV_NOALLOC_SCRATCH_BYTES = 32 << 20  # static scratch of pkv_paged_attention_noalloc, per GPU
+PKV_COUNTER_BYTES = 65536  # arrival counters at the start of every decode workspace (zero between calls)
 
 _c_void_p = ctypes.c_void_p
 _i32 = ctypes.c_int32

@@ -151,35 +151,36 @@ def test_paged_attention_empty_batch_is_a_noop():
 def test_workspace_size_closed_form():
     lib = _lib.lib()
     align = lambda x: (x + 255) // 256 * 256
+    C = _lib.PKV_COUNTER_BYTES  # the arrival counters at the start
     # v1 partitions: the largest of 4096, 2048, ... 256 tokens that still gives
     # 256 workgroups (seqs x units x partitions).
     # Llama-3-8B decode layer: 64 seqs x 8 KV heads at 4096 tokens -> one
     # 4096-token partition already gives 512 workgroups.
     parts = 1
-    assert lib.pkv_paged_attention_workspace_size(64, 32, 8, 128, 4096, 0) == \
+    assert lib.pkv_paged_attention_workspace_size(64, 32, 8, 128, 4096, 0) == C + \
         align(64 * 32 * parts * 2 * 4) + align(64 * 32 * parts * 128 * 4)
     # One Qwen2-7B sequence at 32K (4 units): 512-token partitions, 64 of them.
     parts = 32768 // 512
-    assert lib.pkv_paged_attention_workspace_size(1, 28, 4, 128, 32768, 0) == \
+    assert lib.pkv_paged_attention_workspace_size(1, 28, 4, 128, 32768, 0) == C + \
         align(28 * parts * 2 * 4) + align(28 * parts * 128 * 4)
     # Four sequences at 128K: 4096-token partitions.
     parts = 131072 // 4096
-    assert lib.pkv_paged_attention_workspace_size(4, 28, 4, 128, 131072, 0) == \
+    assert lib.pkv_paged_attention_workspace_size(4, 28, 4, 128, 131072, 0) == C + \
         align(4 * 28 * parts * 2 * 4) + align(4 * 28 * parts * 128 * 4)
     # A short context never goes below 256-token partitions.
-    assert lib.pkv_paged_attention_workspace_size(1, 8, 1, 64, 1000, 0) == \
+    assert lib.pkv_paged_attention_workspace_size(1, 8, 1, 64, 1000, 0) == C + \
         align(8 * 4 * 2 * 4) + align(8 * 4 * 64 * 4)
     # Explicit split-K partitions: runs of them per workgroup, as many as
     # keep v1's grid (here 4096 tokens, so 8 of 512 and 1 of 4096) ...
-    assert lib.pkv_paged_attention_workspace_size(4, 28, 4, 128, 131072, 512) == \
+    assert lib.pkv_paged_attention_workspace_size(4, 28, 4, 128, 131072, 512) == C + \
         align(4 * 28 * 32 * 2 * 4) + align(4 * 28 * 32 * 128 * 4)
-    assert lib.pkv_paged_attention_workspace_size(4, 28, 4, 128, 131072, 4096) == \
+    assert lib.pkv_paged_attention_workspace_size(4, 28, 4, 128, 131072, 4096) == C + \
         align(4 * 28 * 32 * 2 * 4) + align(4 * 28 * 32 * 128 * 4)
     # ... and whole partitions: 10 of 400 tokens (4000) where v1 takes 4096.
-    assert lib.pkv_paged_attention_workspace_size(4, 28, 4, 128, 65536, 400) == \
+    assert lib.pkv_paged_attention_workspace_size(4, 28, 4, 128, 65536, 400) == C + \
         align(4 * 28 * 17 * 2 * 4) + align(4 * 28 * 17 * 128 * 4)
     # One sequence at 32K: v1 takes 512, so 512-token partitions are not grouped.
-    assert lib.pkv_paged_attention_workspace_size(1, 28, 4, 128, 32768, 512) == \
+    assert lib.pkv_paged_attention_workspace_size(1, 28, 4, 128, 32768, 512) == C + \
         align(28 * 64 * 2 * 4) + align(28 * 64 * 128 * 4)
     assert lib.pkv_paged_attention_workspace_size(4, 28, 4, 128, 100, 24) == 0
     assert lib.pkv_paged_attention_workspace_size(4, 28, 3, 128, 100, 0) == 0
@@ -262,3 +263,11 @@ def test_convert_fp8_rejections():
         assert st == code and msg in err, (args, st, err)
     assert lib.pkv_convert_fp8(p(0), p(128), 0, 1.0, 0, 3, None) == _lib.PKV_OK   # empty: no launch
 
+
+
+def test_counter_region_constant_matches_header():
+    import re
+    from pathlib import Path
+    text = (Path(__file__).resolve().parents[1] / "include" / "pagedkv.h").read_text()
+    m = re.search(r"#define PKV_COUNTER_BYTES (\d+)", text)
+    assert m and int(m.group(1)) == _lib.PKV_COUNTER_BYTES

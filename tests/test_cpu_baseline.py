@@ -61,3 +61,30 @@ def test_planted_relayout_mistake_fails():
                                 bs, scale)
     err = np.abs(out.double().numpy() - expected(q, kc, vc, bt, ctx, Hkv, scale, bs)).max()
     assert err > 1e-2
+
+
+def test_scatter_append_matches_oracle():
+    # the append's CPU baseline against the oracle's restatement
+    # (reshape_and_cache_paged5d), float16, with padding and ragged slots
+    rng = np.random.default_rng(11)
+    N, H, D, bs, x, nb = 53, 8, 128, 16, 8, 9
+    k = rng.standard_normal((N, H, D)).astype(np.float16)
+    v = rng.standard_normal((N, H, D)).astype(np.float16)
+    slots = rng.choice(nb * bs, N, replace=False).astype(np.int64)
+    slots[[0, 7, 30]] = -1
+    kc = np.zeros((nb, H, D // x, bs, x), np.float16)
+    vc = np.zeros((nb, H, D, bs), np.float16)
+    kb, vb = (a.view(np.uint16) for a in (k, v))
+    ek, ev = orc.reshape_and_cache_paged5d(kb, vb, kc.view(np.uint16), vc.view(np.uint16), slots, "float16",
+                                           "float16")
+    tk, tv = torch.from_numpy(kc.copy()), torch.from_numpy(vc.copy())
+    cb.scatter_append_paged5d(torch.from_numpy(k), torch.from_numpy(v), tk, tv, torch.from_numpy(slots))
+    assert np.array_equal(tk.numpy().view(np.uint16), ek) and np.array_equal(tv.numpy().view(np.uint16), ev)
+    # a planted mistake (the head dimension split as [x, D/x] instead of
+    # [D/x, x]) is caught
+    keep = torch.from_numpy(slots >= 0)
+    s_ = torch.from_numpy(slots)[keep]
+    bad_k = torch.from_numpy(kc.copy())
+    bad_k.permute(0, 3, 1, 2, 4)[s_ // bs, s_ % bs] = \
+        torch.from_numpy(k)[keep].reshape(-1, H, x, D // x).transpose(2, 3)
+    assert not np.array_equal(bad_k.numpy().view(np.uint16), ek)

@@ -114,12 +114,12 @@ def test_split_k_ignores_unwritten_workspace(D):
     # The merge reads its first step of partials before it knows a row's
     # partition count; entries a row did not write this call (its context is
     # shorter than max_seq_len) must not reach the output, even as NaN.
-    from sglang_mlx_amd import _ext
+    from sglang_mlx_amd import _ext, _lib
     c = make_decode_case(3600 + D, B=3, Hq=8, Hkv=2, D=D, block_size=16, ctx_lo=300, ctx_hi=900,
                          cache_dtype="bfloat16", max_seq_len=4096)
     run(c, partition_size=256)                 # creates the cached workspace
     for scratch in list(_ext._ws_cache.values()):
-        scratch.fill_(0xFF)                    # every float32 word a NaN
+        scratch[_lib.PKV_COUNTER_BYTES:].fill_(0xFF)  # every partition-state word a NaN (counters stay zero)
     torch.cuda.synchronize()
     for ps in (256, None):                     # split-K, and v1 (which splits these few rows too)
         out = run(c, partition_size=ps)
@@ -134,3 +134,28 @@ def test_one_to_two_items_per_workgroup(B):
     c = make_decode_case(3700 + B, B=B, Hq=32, Hkv=8, D=128, block_size=16, ctx_lo=300, ctx_hi=3000,
                          cache_dtype="bfloat16")
     check(c)
+
+
+@pytest.mark.parametrize("case", ["fused_b40", "fused_b1", "deep_b1"])
+def test_fused_merge_leaves_counters_zero(case):
+    # The partition kernel merges its own partitions when a row has at most
+    # 8 (B40 at 2K: 512-token partitions, 4 per row; B1 at 1K: 4 of 256);
+    # deeper rows (B1 at 40K: 80 partitions) take the merge kernel.  v1 and
+    # v2 share the workspace; every call leaves the counter region zero, and
+    # the results hold.
+    from sglang_mlx_amd import _ext, _lib
+    kw = dict(fused_b40=dict(seed=3800, B=40, Hq=8, Hkv=2, ctx_lo=1500, ctx_hi=2000),
+              fused_b1=dict(seed=3801, B=1, Hq=28, Hkv=4, ctx_lo=1024, ctx_hi=1024),
+              deep_b1=dict(seed=3802, B=1, Hq=28, Hkv=4, ctx_lo=40000, ctx_hi=40000))[case]
+    c = make_decode_case(D=128, block_size=16, cache_dtype="bfloat16", **kw)
+    outs = []
+    for ps in (None, 512, None):
+        outs.append(run(c, partition_size=ps))
+        torch.cuda.synchronize()
+        for scratch in _ext._ws_cache.values():
+            assert int(scratch[:_lib.PKV_COUNTER_BYTES].count_nonzero()) == 0
+    a, r = tolerance(c.q_dtype, c.cache_dtype)
+    ref = decode_oracle(c)
+    for out in outs:
+        np.testing.assert_allclose(to_f64(out), ref, atol=a, rtol=r)
+    assert torch.equal(outs[0], outs[2])  # the merge order does not depend on which workgroup merges

@@ -40,7 +40,7 @@ def call(c, t, partition_size, noalloc):
         st = lib.pkv_paged_attention_noalloc(*head, *tail)
     else:
         n = lib.pkv_paged_attention_workspace_size(B, Hq, c.num_kv_heads, D, c.max_seq_len, partition_size)
-        ws = torch.empty(n, dtype=torch.uint8, device="cuda")
+        ws = torch.zeros(n, dtype=torch.uint8, device="cuda")  # counters zero before the first call
         st = lib.pkv_paged_attention(*head, ws.data_ptr(), n, *tail)
     _lib.check(st)
     return out
