@@ -867,13 +867,19 @@ template <int BS, int MAXT> struct WaveBlocks {
   }
   // Block of entry e, for a different e in each lane (entries past the
   // array read entry e % 64 of the first register; the caller ignores them).
+  // Entry e sits in register e / 64 of lane e % 64: every register is read
+  // from that lane and the reader keeps the one its own e names (selecting
+  // the register before the exchange would apply the reader's choice to the
+  // source lane's registers).
   __device__ __forceinline__ int fetch(int e) const {
-    const int c = e >> 6;
-    int x = v[0];
+    const int c = e >> 6, l = e & 63;
+    int x = __shfl(v[0], l);
 #pragma unroll
-    for (int i = 1; i < N; ++i)
-      if (c == i) x = v[i];
-    return __shfl(x, e & 63);
+    for (int i = 1; i < N; ++i) {
+      const int y = __shfl(v[i], l);
+      if (c == i) x = y;
+    }
+    return x;
   }
   // Block of entry e (wave-uniform e).
   __device__ __forceinline__ int get(int e) const {

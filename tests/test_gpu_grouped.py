@@ -260,3 +260,70 @@ def test_fp8_nonfinite_v_in_one_private_tail():
 
 def test_more_than_1024_sequences():
     check(radix_case(6600, B=1100, Hq=8, Hkv=2, D=64, bs=16, prefix_tokens=48, suffix_lo=1, suffix_hi=40))
+
+
+def bound_case(seed, bound, D, bs, fp8=False, q_dtype="bfloat16"):
+    """Contexts that reach the grouped kernel's bound: 256 sequences over 8 KV
+    heads (GQA 4, so 512 items of four sequences: two per CU); 192 share a
+    prefix of bound - 256 tokens and 64 a prefix of bound / 2, each then
+    holds 1-256 private tokens, sequence 0 exactly bound tokens in all.  The
+    block tables are bound tokens wide."""
+    rng = np.random.default_rng(seed)
+    B, Hq, Hkv = 256, 32, 8
+    grp = np.array([0] * 192 + [1] * 64)
+    pre = np.where(grp == 0, bound - 256, bound // 2)
+    tail = rng.integers(1, 257, size=B)
+    tail[0] = 256
+    ctx = (pre + tail).astype(np.int32)
+    nblk = -(-ctx // bs)
+    heads = [pre[0] // bs, pre[-1] // bs]
+    private = nblk - np.array([heads[g] for g in grp])
+    nb = int(sum(heads) + private.sum() + 2)
+    perm = rng.permutation(np.arange(1, nb))
+    shared = [perm[:heads[0]], perm[heads[0]:heads[0] + heads[1]]]
+    pos = heads[0] + heads[1]
+    bt = np.full((B, bound // bs), -1, dtype=np.int32)
+    for s in range(B):
+        h = shared[grp[s]]
+        bt[s, :h.size] = h
+        bt[s, h.size:nblk[s]] = perm[pos:pos + private[s]]
+        pos += private[s]
+    q = normal(rng, (B, Hq, D), q_dtype)
+    c = dict(q=q, bt=bt, ctx=ctx, Hkv=Hkv, bs=bs, qd=q_dtype, alibi=None, scale=1.0 / math.sqrt(D))
+    if fp8:
+        ks, vs = 0.05, 0.02
+        kx = (rng.standard_normal((nb, Hkv, D // 16, bs, 16)) * 1.5).astype(np.float32)
+        vx = (rng.standard_normal((nb, Hkv, D, bs)) * 0.5).astype(np.float32)
+        c.update(kc=orc.fp8_e4m3_encode(kx / np.float32(ks)), vc=orc.fp8_e4m3_encode(vx / np.float32(vs)), dt=FP8,
+                 ks=ks, vs=vs)
+    else:
+        x = X_OF["bfloat16"]
+        c.update(kc=normal(rng, (nb, Hkv, D // x, bs, x), "bfloat16"), vc=normal(rng, (nb, Hkv, D, bs), "bfloat16"),
+                 dt="bfloat16")
+    return c
+
+
+@pytest.mark.parametrize("dt,D,bs,bound", [("bfloat16", 128, 16, 8192), ("bfloat16", 128, 32, 8192),
+                                           ("bfloat16", 64, 8, 8192), ("fp8", 128, 16, 4096),
+                                           ("fp8", 128, 32, 4096), ("fp8", 64, 16, 4096), ("fp8", 64, 8, 4096)])
+def test_group_contexts_at_the_bound(dt, D, bs, bound):
+    # The grouped kernel at the longest contexts its launcher admits (8192
+    # tokens over 16-bit caches, 4096 over FP8 at head sizes 64 and 128):
+    # the job lists, packed tile indices and block ids held in registers at
+    # their fullest, shared and private tiles mixed.  The whole batch runs;
+    # 16 of its rows (the longest among them) are checked against the oracle.
+    fp8 = dt == "fp8"
+    c = bound_case(9100 + D + bs + bound, bound, D, bs, fp8=fp8)
+    scales = dict(k_scale=c["ks"], v_scale=c["vs"]) if fp8 else {}
+    out = kernels.paged_attention_v1(to_torch(c["q"], c["qd"]), to_torch(c["kc"], c["dt"]), to_torch(c["vc"], c["dt"]),
+                                     to_index(c["bt"]), to_index(c["ctx"]), c["Hkv"], c["scale"], bs, bound, None,
+                                     **scales)
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(bound + D + bs)
+    sel = np.concatenate([[0], rng.choice(np.arange(1, 256), size=15, replace=False)])
+    extra = dict(cache_dtype=FP8, k_scale=c["ks"], v_scale=c["vs"]) if fp8 else dict(cache_dtype=c["dt"])
+    exp = orc.paged_attention(c["q"][sel], c["kc"], c["vc"], c["bt"][sel], c["ctx"][sel], c["Hkv"], c["scale"], bs,
+                              bound, None, q_dtype=c["qd"], **extra)
+    a, r = FP8_TOL[c["qd"]] if fp8 else tolerance(c["qd"], c["dt"])
+    assert int(c["ctx"][0]) == bound
+    np.testing.assert_allclose(to_f64(out)[sel], exp, atol=a, rtol=r)

@@ -97,3 +97,68 @@ def test_noalloc_refuses_more_than_its_scratch():
     assert "static scratch" in lib.pkv_last_error().decode()
     torch.cuda.synchronize()
     assert (out == 7.0).all()   # nothing launched
+
+
+CHILD = r'''
+import math
+import torch
+from pkv_cases import make_decode_case
+from pkv_torch import to_index, to_torch
+from sglang_mlx_amd import _lib
+
+lib = _lib.lib()
+# B6 Qwen2-7B heads at 2K-9K tokens: nine partitions per row, merge kernel;
+# B40 at <= 2K over two KV heads: four partitions, merged by the partition
+# kernel with its self-resetting counters in the static array.
+cases = [make_decode_case(8301, B=6, Hq=28, Hkv=4, D=128, block_size=16, ctx_lo=2000, ctx_hi=9000),
+         make_decode_case(8302, B=40, Hq=8, Hkv=2, D=128, block_size=16, ctx_lo=1500, ctx_hi=2000)]
+ts = [(to_torch(c.q, c.q_dtype), to_torch(c.k_cache, c.cache_dtype), to_torch(c.v_cache, c.cache_dtype),
+       to_index(c.block_tables), to_index(c.context_lens)) for c in cases]
+
+
+def call(c, t, out, stream):
+    q, kc, vc, bt, lens = t
+    B, Hq, D = q.shape
+    return lib.pkv_paged_attention_noalloc(
+        out.data_ptr(), q.data_ptr(), kc.data_ptr(), vc.data_ptr(), bt.data_ptr(), lens.data_ptr(), None,
+        B, Hq, c.num_kv_heads, D, c.block_size, bt.shape[1], c.max_seq_len, kc.shape[0], c.scale, q.stride(0),
+        kc.stride(0), kc.stride(1), vc.stride(0), vc.stride(1), _lib.PKV_LAYOUT_PAGED5D, 0,
+        _lib.PKV_BF16, _lib.PKV_BF16, 1.0, 1.0, stream)
+
+
+torch.cuda.synchronize()
+outs = [torch.full_like(t[0], float("nan")) for t in ts]
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph):  # this process's first calls on the device are captured
+    for c, t, o in zip(cases, ts, outs):
+        assert call(c, t, o, torch.cuda.current_stream().cuda_stream) == 0, lib.pkv_last_error()
+torch.cuda.synchronize()
+for replay in range(4):
+    for o in outs:
+        o.fill_(float("nan"))
+    graph.replay()
+    torch.cuda.synchronize()
+    for c, t, o in zip(cases, ts, outs):
+        eager = torch.full_like(t[0], float("nan"))
+        assert call(c, t, eager, torch.cuda.current_stream().cuda_stream) == 0, lib.pkv_last_error()
+        torch.cuda.synchronize()
+        assert torch.equal(o, eager), ("replay", replay)
+        assert not torch.isnan(o.float()).any()
+print("graph replays equal the eager calls")
+'''
+
+
+def test_noalloc_under_graph_capture_in_a_fresh_process():
+    # The entry point that allocates nothing, captured in a HIP graph by a
+    # process whose first call on the GPU is the captured one (the static
+    # array's address is looked up inside the capture), replayed four times
+    # with eager calls in between, each replay bit-equal to the eager call.
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, PYTHONPATH=os.pathsep.join([os.path.join(root, "sglang-mlx_amd"),
+                                                       os.path.join(root, "tests"), root]))
+    r = subprocess.run([sys.executable, "-c", CHILD], env=env, capture_output=True, text=True, timeout=240)
+    assert r.returncode == 0, r.stdout[-2000:] + r.stderr[-4000:]
+    assert "graph replays equal the eager calls" in r.stdout
