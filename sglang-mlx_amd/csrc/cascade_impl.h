@@ -50,7 +50,11 @@ constexpr int kCascadeWaves = 4;                               // wavefronts per
 constexpr int kPrefixSets = 2;                                 // 16-column query sets per wavefront
 constexpr int kPrefixRows = kCascadeWaves * kPrefixSets * 16;  // query rows per prefix workgroup
 constexpr int kPrefixStageTiles = 2;                           // 16-token tiles per LDS stage (one pair)
-constexpr int kPrefixBuffers = 3;                              // LDS stage buffers
+// LDS stage buffers (NB - 1 stages in flight).  Four (three stages ahead)
+// timed the same for the prefix pass alone (35.7 against 35.6 us on the
+// radix-shared B256 workload) and cost the FP8 cascade 2.7 us (LDS 67.6
+// instead of 51 KB per workgroup).
+constexpr int kPrefixBuffers = 3;
 constexpr int kTailBuffers = 2;                                // tile buffers per tail wavefront
 
 // Largest block-table span of one prefix chunk (8-token blocks).
@@ -281,7 +285,8 @@ template <class QT, class CT, int D, int BS>
 __device__ __forceinline__ void prefix_role(const DecodeParams& p, const CascadeParams& c, int wi, int kvh,
                                             uint4 (*s_buf0)[PrefixTile<CT, D>::kUnits],
                                             uint4 (*s_buf1)[PrefixTile<CT, D>::kUnits],
-                                            uint4 (*s_buf2)[PrefixTile<CT, D>::kUnits], int32_t* s_blk,
+                                            uint4 (*s_buf2)[PrefixTile<CT, D>::kUnits],
+                                            uint4 (*s_buf3)[PrefixTile<CT, D>::kUnits], int32_t* s_blk,
                                             uint32_t (*s_live)[kPrefixStageTiles]) {
   using MT = typename MmaOf<QT, CT>::type;
   using CS = typename Elem<CT>::storage;
@@ -340,7 +345,8 @@ __device__ __forceinline__ void prefix_role(const DecodeParams& p, const Cascade
   auto buffer = [&](auto k) __attribute__((always_inline)) -> uint4 (*)[PT::kUnits] {
     if constexpr (decltype(k)::value == 0) return s_buf0;
     else if constexpr (decltype(k)::value == 1) return s_buf1;
-    else return s_buf2;
+    else if constexpr (decltype(k)::value == 2) return s_buf2;
+    else return s_buf3;
   };
   // Wavefront w stages part w % 2 (K, V) of tile w / 2 of a stage.
   const int my_tile = wave >> 1, my_part = wave & 1;
@@ -363,9 +369,13 @@ __device__ __forceinline__ void prefix_role(const DecodeParams& p, const Cascade
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
   using I2 = std::integral_constant<int, 2>;
-  static_assert(kPrefixBuffers == 3, "three stage buffers");
+  using I3 = std::integral_constant<int, 3>;
+  constexpr int NB = kPrefixBuffers;
+  static_assert(NB == 3 || NB == 4, "three or four stage buffers");
   stage(I0{}, 0);
   if (1 < nstages) stage(I1{}, 1);
+  if constexpr (NB == 4)
+    if (2 < nstages) stage(I2{}, 2);
 
   // Scores are scale * q.k in the log2 domain.  A negative scale is folded
   // into the query's sign bits (exact), so the softmax sees scale >= 0 and
@@ -487,39 +497,48 @@ __device__ __forceinline__ void prefix_role(const DecodeParams& p, const Cascade
   };
   // Direct-to-LDS loads a wavefront issues per stage; s_waitcnt immediates
   // (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt in 6:4 left at its
-  // maximum, lgkmcnt 0) that leave 0 or 1 later stage's loads in flight.
+  // maximum, lgkmcnt 0) that leave 0, 1 or 2 later stages' loads in flight.
   constexpr int LPS = PT::kKUnits / 64 * (BS >= kTile ? 1 : 2);
-  static_assert(LPS < 64, "vmcnt counts at most 63 loads");
+  static_assert(2 * LPS < 64, "vmcnt counts at most 63 loads");
   constexpr int kWait0 = (7 << 4);
   constexpr int kWait1 = (LPS & 15) | ((LPS >> 4) << 14) | (7 << 4);
+  constexpr int kWait2 = ((2 * LPS) & 15) | (((2 * LPS) >> 4) << 14) | (7 << 4);
   // The workgroup meets at a bare s_barrier (a __syncthreads, or any
   // workgroup fence that covers LDS, waits for every outstanding
-  // direct-to-LDS load, the stage in flight included).  Each wavefront
+  // direct-to-LDS load, the stages in flight included).  Each wavefront
   // first waits explicitly for its own loads of the next stage and its LDS
   // writes (the kWait* immediates); the asm's memory clobber keeps the
   // compiler from moving memory accesses across the barrier.
   auto barrier = [] __attribute__((always_inline)) { asm volatile("s_barrier" ::: "memory"); };
-  __builtin_amdgcn_s_waitcnt(kWait0);  // stages 0 and 1, and the queries
+  __builtin_amdgcn_s_waitcnt(kWait0);  // the first stages, and the queries
   barrier();
-  // Step k of a turn consumes stage st (buffer k), issues stage st + 2 into
-  // the buffer consumed one step earlier, waits for stage st + 1 and meets
-  // the workgroup at a barrier.
+  // Step k of a turn consumes stage st (buffer k), issues stage st + NB - 1
+  // into the buffer consumed one step earlier, waits for stage st + 1 (the
+  // stages after it may stay in flight) and meets the workgroup at a
+  // barrier.
   auto step = [&](auto k, int st) __attribute__((always_inline)) {
     constexpr int K = decltype(k)::value;
-    if (st + 2 < nstages) stage(std::integral_constant<int, (K + 2) % 3>{}, st + 2);
+    if (st + NB - 1 < nstages) stage(std::integral_constant<int, (K + NB - 1) % NB>{}, st + NB - 1);
     consume_pair(buffer(k)[0], buffer(k)[1], s_live[K][0], s_live[K][1], t0 + st * ST * kTile);
-    if (st + 2 < nstages)
+    const int later = min(NB - 2, nstages - 2 - st);  // stages issued after st + 1
+    if (later >= 2)
+      __builtin_amdgcn_s_waitcnt(kWait2);
+    else if (later == 1)
       __builtin_amdgcn_s_waitcnt(kWait1);
     else
       __builtin_amdgcn_s_waitcnt(kWait0);
     barrier();
   };
-  for (int st = 0; st < nstages; st += 3) {
+  for (int st = 0; st < nstages; st += NB) {
     step(I0{}, st);
     if (st + 1 >= nstages) break;
     step(I1{}, st + 1);
     if (st + 2 >= nstages) break;
     step(I2{}, st + 2);
+    if constexpr (NB == 4) {
+      if (st + 3 >= nstages) break;
+      step(I3{}, st + 3);
+    }
   }
 
   // Partial states: each row's true maximum, its weight sum against it and
@@ -632,6 +651,11 @@ __global__ __launch_bounds__(64 * kCascadeWaves, 2) void paged_cascade_kernel(De
   __shared__ uint4 s_buf0[kPrefixStageTiles][PT::kUnits];
   __shared__ uint4 s_buf1[kPrefixStageTiles][PT::kUnits];
   __shared__ uint4 s_buf2[kPrefixStageTiles][PT::kUnits];
+  uint4 (*s_buf3p)[PT::kUnits] = s_buf2;  // unused with three buffers
+  if constexpr (kPrefixBuffers == 4) {
+    __shared__ uint4 s_buf3[kPrefixStageTiles][PT::kUnits];
+    s_buf3p = s_buf3;
+  }
   __shared__ int32_t s_blk[kPrefixMaxBlocks];
   __shared__ uint32_t s_live[kPrefixBuffers][kPrefixStageTiles];
   const int prefix_wgs = c.num_tiles * p.num_kv_heads;
@@ -641,7 +665,7 @@ __global__ __launch_bounds__(64 * kCascadeWaves, 2) void paged_cascade_kernel(De
     // sharing their SIMDs.
     __builtin_amdgcn_s_setprio(3);
     prefix_role<QT, CT, D, BS>(p, c, (int)blockIdx.x / p.num_kv_heads, (int)blockIdx.x % p.num_kv_heads, s_buf0,
-                               s_buf1, s_buf2, s_blk, s_live);
+                               s_buf1, s_buf2, s_buf3p, s_blk, s_live);
   } else {
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int tail_wgs = (int)gridDim.x - prefix_wgs;
