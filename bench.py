@@ -828,6 +828,10 @@ def main():
     else:
         line["cpu_baseline"] = None
     print(json.dumps(line), flush=True)
+    # Leave nothing queued or cached on the device when the interpreter
+    # tears down (graphs and pools of every leg are released here).
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
 
 
 if __name__ == "__main__":

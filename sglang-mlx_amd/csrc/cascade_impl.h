@@ -280,14 +280,56 @@ __device__ __forceinline__ int tail_parts(const CascadeParams& c, int tail) {
   return tail <= c.part_tokens ? 1 : (tail + c.part_tokens - 1) / c.part_tokens;
 }
 
+// FP8 stages are dequantised once, by the whole workgroup, into a 16-bit
+// image of the stage in MT's layout (PrefixTile<MT, D>) that every
+// wavefront then reads as it would a 16-bit cache's stage: thread t takes
+// code units t, t + NT, ... of the stage's two tiles (K unit c16 * 16 + tk ->
+// image units (2 c16) * 16 + tk and (2 c16 + 1) * 16 + tk; V unit d -> image
+// units 2 d and 2 d + 1).  Exponent-15 codes take the exact path (one
+// wave-wide test).  Conversion per wavefront and tile pair drops to a quarter
+// of what reading the codes in every wavefront costs.
+template <class MT, int D, int NT>
+__device__ __forceinline__ void convert_stage(const uint4 (*codes)[PrefixTile<FP8, D>::kUnits],
+                                              uint4 (*img)[PrefixTile<MT, D>::kUnits], int tid) {
+  constexpr int CU = PrefixTile<FP8, D>::kUnits;  // code units per tile: D of K, D of V
+  constexpr int IK = PrefixTile<MT, D>::kKUnits;  // image K units per tile (2 D)
+  static_assert((kPrefixStageTiles * CU) % NT == 0, "whole code units per thread");
+#pragma unroll
+  for (int u0 = 0; u0 < kPrefixStageTiles * CU; u0 += NT) {
+    const int u = u0 + tid;
+    const int tile = u / CU, r = u - tile * CU;
+    const uint4 w = codes[tile][r];
+    const uint32_t probe = fp8x4_special(w.x) | fp8x4_special(w.y) | fp8x4_special(w.z) | fp8x4_special(w.w);
+    const bool special = __any(probe != 0u);
+    auto cvt = [&](uint32_t x) __attribute__((always_inline)) {
+      return special ? fp8x4_exact<MT>(x) : fp8x4_cvt<MT>(x);
+    };
+    const uint2 a = cvt(w.x), b = cvt(w.y), c = cvt(w.z), d = cvt(w.w);
+    int i0, i1;
+    if (r < D) {  // K: dimensions 16 c16 .. +15 of token tk
+      const int c16 = r >> 4, tk = r & 15;
+      i0 = (2 * c16) * 16 + tk;
+      i1 = i0 + 16;
+    } else {      // V: tokens 0 .. 15 of dimension r - D
+      i0 = IK + 2 * (r - D);
+      i1 = i0 + 1;
+    }
+    img[tile][i0] = make_uint4(a.x, a.y, b.x, b.y);
+    img[tile][i1] = make_uint4(c.x, c.y, d.x, d.y);
+  }
+}
+
 // Prefix role: plan tile `wi`, KV head `kvh` (see the file comment).
 template <class QT, class CT, int D, int BS>
 __device__ __forceinline__ void prefix_role(const DecodeParams& p, const CascadeParams& c, int wi, int kvh,
                                             uint4 (*s_buf0)[PrefixTile<CT, D>::kUnits],
                                             uint4 (*s_buf1)[PrefixTile<CT, D>::kUnits],
                                             uint4 (*s_buf2)[PrefixTile<CT, D>::kUnits],
-                                            uint4 (*s_buf3)[PrefixTile<CT, D>::kUnits], int32_t* s_blk,
-                                            uint32_t (*s_live)[kPrefixStageTiles]) {
+                                            uint4 (*s_buf3)[PrefixTile<CT, D>::kUnits],
+                                            uint4 (*s_img0)[PrefixTile<typename MmaOf<QT, CT>::type, D>::kUnits],
+                                            uint4 (*s_img1)[PrefixTile<typename MmaOf<QT, CT>::type, D>::kUnits],
+                                            int32_t* s_blk, uint32_t (*s_live)[kPrefixStageTiles],
+                                            uint32_t (*s_ilive)[kPrefixStageTiles]) {
   using MT = typename MmaOf<QT, CT>::type;
   using CS = typename Elem<CT>::storage;
   using PT = PrefixTile<CT, D>;
@@ -374,7 +416,7 @@ __device__ __forceinline__ void prefix_role(const DecodeParams& p, const Cascade
   static_assert(NB == 3 || NB == 4, "three or four stage buffers");
   stage(I0{}, 0);
   if (1 < nstages) stage(I1{}, 1);
-  if constexpr (NB == 4)
+  if constexpr (NB == 4 && !PT::kF8)  // FP8 stages through two code buffers
     if (2 < nstages) stage(I2{}, 2);
 
   // Scores are scale * q.k in the log2 domain.  A negative scale is folded
@@ -417,10 +459,13 @@ __device__ __forceinline__ void prefix_role(const DecodeParams& p, const Cascade
   // step over their 32 tokens, P V^T on 16x16x32 MFMAs.  Each phase runs
   // for both query sets before the next, so that the two sets' dependent
   // chains (MFMA results -> softmax -> MFMA operands) interleave.
-  auto consume_pair = [&](const uint4* ta, const uint4* tb, uint32_t live_a, uint32_t live_b,
+  // img: the pair is a 16-bit image of an FP8 stage (MT's layout) rather
+  // than the stage as loaded.
+  auto consume_pair = [&](auto img, const uint4* ta, const uint4* tb, uint32_t live_a, uint32_t live_b,
                           int tok_a) __attribute__((always_inline)) {
-    PrefixOperands<CT, MT, D> op;
-    read_pair<CT, MT, D>(op, ta, tb, lane, g, col);
+    using OT = std::conditional_t<decltype(img)::value, MT, CT>;
+    PrefixOperands<OT, MT, D> op;
+    read_pair<OT, MT, D>(op, ta, tb, lane, g, col);
     const int va = tok_a + 4 * g, vb = va + kTile;
     f32x4 sa[NS], sb[NS];
 #pragma unroll
@@ -510,8 +555,48 @@ __device__ __forceinline__ void prefix_role(const DecodeParams& p, const Cascade
   // writes (the kWait* immediates); the asm's memory clobber keeps the
   // compiler from moving memory accesses across the barrier.
   auto barrier = [] __attribute__((always_inline)) { asm volatile("s_barrier" ::: "memory"); };
+  // lgkmcnt(0) alone: this wavefront's LDS writes done, its loads in flight
+  // left so.
+  constexpr int kWaitLds = 15 | (7 << 4) | (3 << 14);
   __builtin_amdgcn_s_waitcnt(kWait0);  // the first stages, and the queries
   barrier();
+  if constexpr (PT::kF8) {
+    // Two code buffers and two images: step st consumes image st % 2, issues
+    // stage st + 2 into code buffer st % 2 (its codes became image st % 2 a
+    // step earlier), waits for stage st + 1, and the workgroup converts it
+    // into the other image.  Each image carries its stage's live-token masks
+    // (s_ilive), since the next stage issued into a code buffer rewrites
+    // that buffer's masks before the image is consumed.
+    auto img = [&](auto k) __attribute__((always_inline)) -> uint4 (*)[PrefixTile<MT, D>::kUnits] {
+      if constexpr (decltype(k)::value == 0) return s_img0;
+      else return s_img1;
+    };
+    auto convert = [&](auto k) __attribute__((always_inline)) {
+      convert_stage<MT, D, NT>(buffer(k), img(k), tid);
+      if (tid < ST) s_ilive[decltype(k)::value][tid] = s_live[decltype(k)::value][tid];
+      __builtin_amdgcn_s_waitcnt(kWaitLds);
+      barrier();
+    };
+    convert(I0{});
+    auto fstep = [&](auto k, int st) __attribute__((always_inline)) {
+      constexpr int K = decltype(k)::value;
+      using KN = std::integral_constant<int, K ^ 1>;
+      if (st + 2 < nstages) stage(k, st + 2);
+      consume_pair(std::true_type{}, img(k)[0], img(k)[1], s_ilive[K][0], s_ilive[K][1], t0 + st * ST * kTile);
+      if (st + 2 < nstages)
+        __builtin_amdgcn_s_waitcnt(kWait1);
+      else
+        __builtin_amdgcn_s_waitcnt(kWait0);
+      barrier();
+      if (st + 1 < nstages) convert(KN{});
+    };
+    for (int st = 0; st < nstages; st += 2) {
+      fstep(I0{}, st);
+      if (st + 1 >= nstages) break;
+      fstep(I1{}, st + 1);
+    }
+  } else {
+
   // Step k of a turn consumes stage st (buffer k), issues stage st + NB - 1
   // into the buffer consumed one step earlier, waits for stage st + 1 (the
   // stages after it may stay in flight) and meets the workgroup at a
@@ -519,7 +604,8 @@ __device__ __forceinline__ void prefix_role(const DecodeParams& p, const Cascade
   auto step = [&](auto k, int st) __attribute__((always_inline)) {
     constexpr int K = decltype(k)::value;
     if (st + NB - 1 < nstages) stage(std::integral_constant<int, (K + NB - 1) % NB>{}, st + NB - 1);
-    consume_pair(buffer(k)[0], buffer(k)[1], s_live[K][0], s_live[K][1], t0 + st * ST * kTile);
+    consume_pair(std::false_type{}, buffer(k)[0], buffer(k)[1], s_live[K][0], s_live[K][1],
+                   t0 + st * ST * kTile);
     const int later = min(NB - 2, nstages - 2 - st);  // stages issued after st + 1
     if (later >= 2)
       __builtin_amdgcn_s_waitcnt(kWait2);
@@ -539,6 +625,8 @@ __device__ __forceinline__ void prefix_role(const DecodeParams& p, const Cascade
       if (st + 3 >= nstages) break;
       step(I3{}, st + 3);
     }
+  }
+
   }
 
   // Partial states: each row's true maximum, its weight sum against it and
@@ -648,14 +736,29 @@ __global__ __launch_bounds__(64 * kCascadeWaves, 2) void paged_cascade_kernel(De
   using PT = PrefixTile<CT, D>;
   static_assert(D % 64 == 0, "head sizes 64 and 128");
   static_assert(!std::is_same<QT, F32>::value, "the cascade takes a 16-bit query");
+  using IT = PrefixTile<typename MmaOf<QT, CT>::type, D>;
+  // Stage buffers: three (or four) of the stages as loaded for 16-bit
+  // caches; for FP8 two of codes plus two 16-bit images.
   __shared__ uint4 s_buf0[kPrefixStageTiles][PT::kUnits];
   __shared__ uint4 s_buf1[kPrefixStageTiles][PT::kUnits];
-  __shared__ uint4 s_buf2[kPrefixStageTiles][PT::kUnits];
-  uint4 (*s_buf3p)[PT::kUnits] = s_buf2;  // unused with three buffers
-  if constexpr (kPrefixBuffers == 4) {
-    __shared__ uint4 s_buf3[kPrefixStageTiles][PT::kUnits];
-    s_buf3p = s_buf3;
+  uint4 (*s_buf2p)[PT::kUnits] = s_buf1;
+  uint4 (*s_buf3p)[PT::kUnits] = s_buf1;  // unused unless four buffers
+  uint4 (*s_img0p)[IT::kUnits] = nullptr;
+  uint4 (*s_img1p)[IT::kUnits] = nullptr;
+  if constexpr (PT::kF8) {
+    __shared__ uint4 s_img0[kPrefixStageTiles][IT::kUnits];
+    __shared__ uint4 s_img1[kPrefixStageTiles][IT::kUnits];
+    s_img0p = s_img0;
+    s_img1p = s_img1;
+  } else {
+    __shared__ uint4 s_buf2[kPrefixStageTiles][PT::kUnits];
+    s_buf2p = s_buf2;
+    if constexpr (kPrefixBuffers == 4) {
+      __shared__ uint4 s_buf3[kPrefixStageTiles][PT::kUnits];
+      s_buf3p = s_buf3;
+    }
   }
+  __shared__ uint32_t s_ilive[2][kPrefixStageTiles];
   __shared__ int32_t s_blk[kPrefixMaxBlocks];
   __shared__ uint32_t s_live[kPrefixBuffers][kPrefixStageTiles];
   const int prefix_wgs = c.num_tiles * p.num_kv_heads;
@@ -665,7 +768,7 @@ __global__ __launch_bounds__(64 * kCascadeWaves, 2) void paged_cascade_kernel(De
     // sharing their SIMDs.
     __builtin_amdgcn_s_setprio(3);
     prefix_role<QT, CT, D, BS>(p, c, (int)blockIdx.x / p.num_kv_heads, (int)blockIdx.x % p.num_kv_heads, s_buf0,
-                               s_buf1, s_buf2, s_buf3p, s_blk, s_live);
+                               s_buf1, s_buf2p, s_buf3p, s_img0p, s_img1p, s_blk, s_live, s_ilive);
   } else {
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int tail_wgs = (int)gridDim.x - prefix_wgs;
