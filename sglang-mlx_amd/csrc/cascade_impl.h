@@ -302,7 +302,7 @@ __device__ __forceinline__ void convert_stage(const uint4 (*codes)[PrefixTile<FP
     const uint32_t probe = fp8x4_special(w.x) | fp8x4_special(w.y) | fp8x4_special(w.z) | fp8x4_special(w.w);
     const bool special = __any(probe != 0u);
     auto cvt = [&](uint32_t x) __attribute__((always_inline)) {
-      return special ? fp8x4_exact<MT>(x) : fp8x4_cvt<MT>(x);
+      return special ? fp8x4_exact_inline<MT>(x) : fp8x4_cvt<MT>(x);
     };
     const uint2 a = cvt(w.x), b = cvt(w.y), c = cvt(w.z), d = cvt(w.w);
     int i0, i1;

@@ -96,4 +96,19 @@ template <class MT> __device__ __forceinline__ uint2 fp8x4_exact(uint32_t w) {
   return r;
 }
 
+// fp8x4_exact without the out-of-line fix-up (selects instead of a call),
+// for code that holds many values live where the call would make the
+// compiler save them to scratch.
+template <class MT> __device__ __forceinline__ uint2 fp8x4_exact_inline(uint32_t w) {
+  const uint2 r = fp8x4_cvt<MT>(w);
+  uint32_t h[4] = {r.x & 0xffffu, r.x >> 16, r.y & 0xffffu, r.y >> 16};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t c = (w >> (8 * i)) & 0xffu;
+    const uint32_t fix = (c & 7u) ? Special16<MT>::kNaN : (Special16<MT>::kInf | ((c & 0x80u) << 8));
+    h[i] = ((c >> 3) & 15u) == 15u ? fix : h[i];
+  }
+  return make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+}
+
 }  // namespace pkv
