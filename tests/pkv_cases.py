@@ -125,6 +125,45 @@ def make_append_case(seed: int, N: int, H: int, D: int, num_slots: int, block_si
     return AppendCase(key, value, slots.astype(np.int32), num_slots, block_size, kv_dtype, cache_dtype)
 
 
+def run_slots(rng, N: int, num_blocks: int, block_size: int, pad_frac: float = 0.03) -> np.ndarray:
+    """N unique slots laid out as a prefill and its neighbours write them:
+    blocks in a shuffled order, each taken whole (a run of block_size
+    consecutive slots, half the blocks), as a run over part of the block
+    (a quarter) or as one slot (a quarter); then pad_frac of the tokens set
+    to -1.  Needs num_blocks large enough to hold N tokens (~10 per block)."""
+    slots: list[int] = []
+    for b in rng.permutation(num_blocks):
+        if len(slots) >= N:
+            break
+        kind = int(rng.integers(0, 4))
+        base = int(b) * block_size
+        if kind < 2:
+            slots.extend(range(base, base + block_size))
+        elif kind == 2:
+            lo = int(rng.integers(0, block_size))
+            slots.extend(range(base + lo, base + int(rng.integers(lo + 1, block_size + 1))))
+        else:
+            slots.append(base + int(rng.integers(0, block_size)))
+    if len(slots) < N:
+        raise ValueError("too few blocks for N tokens")
+    out = np.asarray(slots[:N], dtype=np.int64)
+    npad = int(round(pad_frac * N))
+    if npad:
+        out[rng.choice(N, size=npad, replace=False)] = -1
+    return out.astype(np.int32)
+
+
+def make_run_append_case(seed: int, N: int, H: int, D: int, num_blocks: int, block_size: int,
+                         kv_dtype: str = "bfloat16", cache_dtype: str | None = None) -> AppendCase:
+    """An append whose slots come in runs (run_slots)."""
+    cache_dtype = cache_dtype or kv_dtype
+    rng = np.random.default_rng(seed)
+    slots = run_slots(rng, N, num_blocks, block_size)
+    key = normal(rng, (N, H, D), kv_dtype)
+    value = normal(rng, (N, H, D), kv_dtype)
+    return AppendCase(key, value, slots, num_blocks * block_size, block_size, kv_dtype, cache_dtype)
+
+
 def tolerance(q_dtype: str, cache_dtype: str) -> tuple[float, float]:
     """(atol, rtol) of the attention outputs: 2e-3/1e-2 for float16,
     1e-2/2e-2 for bfloat16 (the coarser of query and cache type decides)."""

@@ -12,6 +12,7 @@ import pytest
 import torch
 
 from oracle import pagedkv_oracle as orc
+from pkv_cases import run_slots
 from pkv_torch import to_index, to_numpy, to_torch
 from sglang_mlx_amd import kernels, _ext
 
@@ -53,6 +54,25 @@ def test_paged5d(kv_dtype, bs, scales):
     assert out[0] is kc
     torch.cuda.synchronize()
     rk, rv = orc.reshape_and_cache_paged5d(key, value, kc0, vc0, slots, kv_dtype, FP8, *scales)
+    np.testing.assert_array_equal(to_numpy(kc), rk)
+    np.testing.assert_array_equal(to_numpy(vc), rv)
+
+
+@pytest.mark.parametrize("kv_dtype", ["float32", "bfloat16"])
+def test_paged5d_large_append_of_slot_runs(kv_dtype):
+    # 4096 tokens x 8 heads x D 128: 8 MiB of codes written, the size from
+    # which tokens inside runs of consecutive slots are stored nontemporally.
+    H, D, nb, bs = 8, 128, 1024, 16
+    rng = np.random.default_rng(77)
+    slots = run_slots(rng, 4096, nb, bs)
+    key, value = wide_values(rng, (4096, H, D), kv_dtype), wide_values(rng, (4096, H, D), kv_dtype)
+    kc0 = rng.integers(0, 256, size=(nb, H, D // 16, bs, 16), dtype=np.uint8)
+    vc0 = rng.integers(0, 256, size=(nb, H, D, bs), dtype=np.uint8)
+    kc, vc = to_torch(kc0, FP8), to_torch(vc0, FP8)
+    kernels.reshape_and_cache(to_torch(key, kv_dtype), to_torch(value, kv_dtype), kc, vc, to_index(slots),
+                              k_scale=0.37, v_scale=1.7)
+    torch.cuda.synchronize()
+    rk, rv = orc.reshape_and_cache_paged5d(key, value, kc0, vc0, slots, kv_dtype, FP8, 0.37, 1.7)
     np.testing.assert_array_equal(to_numpy(kc), rk)
     np.testing.assert_array_equal(to_numpy(vc), rv)
 

@@ -3,8 +3,10 @@
 Cases: the reference test's fixture geometry and shape sweep
 (tests/test_paged_attention_kernel.py:138-210, :248-282), every
 (kv dtype -> cache dtype) pair of reshape_and_cache.metal:91-95 in both
-layouts, strided and misaligned sources, padding-only and empty batches, and
-the 4096-token append workload at full size (65,536 slots, 5% padding).
+layouts, strided and misaligned sources, padding-only and empty batches,
+the 4096-token append workload at full size (65,536 slots, 5% padding), and
+appends large enough (at least 8 MiB of cache written) that their runs of
+consecutive slots take the nontemporal store path.
 Caches start from random bits so untouched slots are checked too.
 """
 
@@ -13,7 +15,7 @@ import pytest
 import torch
 
 from oracle import pagedkv_oracle as orc
-from pkv_cases import X_OF, make_append_case
+from pkv_cases import X_OF, make_append_case, make_run_append_case
 from pkv_torch import to_index, to_numpy, to_torch
 from sglang_mlx_amd import _ext
 
@@ -209,3 +211,18 @@ def test_append_workload_full_size(layout):
         check_token_major(case, 8, 128)
     else:
         check_paged5d(case, 4096, 8, 128)
+
+
+@pytest.mark.parametrize("kv_dtype,cache_dtype", [("bfloat16", "bfloat16"), ("float16", "float16"),
+                                                  ("float32", "float32"), ("float32", "bfloat16")])
+def test_large_append_of_slot_runs(kv_dtype, cache_dtype):
+    # 4096 tokens x 8 heads x D 128: 16 MiB (32 MiB for float32 caches) of
+    # cache written, above the 8 MiB from which tokens inside runs of
+    # consecutive slots are stored nontemporally; scattered tokens and
+    # padding in the same launch take the default stores.
+    case = make_run_append_case(31, N=4096, H=8, D=128, num_blocks=1024, block_size=16,
+                                kv_dtype=kv_dtype, cache_dtype=cache_dtype)
+    s = case.slot_mapping
+    in_run = (s[1:] == s[:-1] + 1) & (s[:-1] >= 0)
+    assert in_run.mean() > 0.5 and (~in_run).sum() > 100
+    check_paged5d(case, 1024, 8, 128)
