@@ -268,10 +268,14 @@ __device__ __forceinline__ void fold_states(WaveAcc<D>& acc, const CascadeParams
 // the context is then streamed whole.  The tail and merge kernels decide
 // alike.
 template <int BS>
-__device__ __forceinline__ int usable_prefix(const CascadeParams& c, int seq, bool live) {
+__device__ __forceinline__ int usable_prefix_of(const CascadeParams& c, int plan_len, bool live) {
   constexpr int ALIGN = BS < kTile ? BS : kTile;  // a tail starts on a tile boundary of its blocks
-  const int pre = live ? c.prefix_lens[seq] : 0;
+  const int pre = live ? plan_len : 0;
   return (pre < 0 || pre % ALIGN != 0 || pre > c.max_chunks * c.chunk) ? 0 : pre;
+}
+template <int BS>
+__device__ __forceinline__ int usable_prefix(const CascadeParams& c, int seq, bool live) {
+  return usable_prefix_of<BS>(c, live ? c.prefix_lens[seq] : 0, live);
 }
 
 // Tail partitions of a sequence whose tail (tokens after the prefix) is
@@ -782,21 +786,52 @@ template <class QT, int D, int BS>
 __global__ __launch_bounds__(64) void paged_cascade_merge_kernel(DecodeParams p, CascadeParams c) {
   using QS = typename Elem<QT>::storage;
   constexpr int kStates = 6;  // states whose loads are in flight together
+  constexpr int DT = Tile<D>::DT;
   const int lane = threadIdx.x;
   const int g = lane >> 4, col = lane & 15;
-  const int64_t row = (int64_t)blockIdx.x * 16 + col;
-  bool on = row < (int64_t)p.num_seqs * p.num_heads;
-  const int seq = on ? (int)(row / p.num_heads) : 0;
+  const int64_t row0 = (int64_t)blockIdx.x * 16 + col;
+  bool on = row0 < (int64_t)p.num_seqs * p.num_heads;
+  const int64_t row = on ? row0 : 0;
+  const int seq = (int)(row / p.num_heads);
+  // The row's first tail-partition state and first prefix-chunk state are
+  // loaded together with its context and prefix lengths, in one round trip
+  // instead of three: both slots exist for every row, and each is folded
+  // below only if the row has it (a slot this call did not write may hold
+  // inf or NaN).  The fold order is unchanged: tail partitions, then chunks.
   const uint32_t ctx = (uint32_t)p.context_lens[seq];
+  const int plan_len = c.prefix_lens[seq];
+  const float2 ml_t = *reinterpret_cast<const float2*>(c.ws_tail_ml + row * c.max_parts * 2);
+  const float2 ml_c = *reinterpret_cast<const float2*>(c.ws_ml + row * c.max_chunks * 2);
+  float4 o_t[DT], o_c[DT];
+  {
+    const float* wt = c.ws_tail_o + row * c.max_parts * D + 4 * g;
+    const float* wc = c.ws_o + row * c.max_chunks * D + 4 * g;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      o_t[dt] = *reinterpret_cast<const float4*>(wt + 16 * dt);
+      o_c[dt] = *reinterpret_cast<const float4*>(wc + 16 * dt);
+    }
+    // The asm takes every one of those values, so all the loads are issued
+    // before it; without it the compiler moves the state loads past the
+    // branches on the lengths.
+    float anchor = ml_t.x + ml_t.y + ml_c.x + ml_c.y;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) anchor += o_t[dt].x + o_t[dt].y + o_t[dt].z + o_t[dt].w + o_c[dt].x + o_c[dt].y +
+                                              o_c[dt].z + o_c[dt].w;
+    asm volatile("" ::"v"(anchor), "v"(ctx), "v"(plan_len));
+  }
   const bool live = ctx != 0 && ctx <= (uint32_t)p.max_seq_len;
-  const int pre = usable_prefix<BS>(c, seq, live);
+  const int pre = usable_prefix_of<BS>(c, plan_len, live);
   const int np = tail_parts(c, live ? (int)ctx - min(pre, (int)ctx) : 0);
   on = on && !(pre == 0 && np == 1);  // rows the tail role wrote
-  const int nt = min(np, c.max_parts);
+  const int nt = min(np, c.max_parts);  // >= 1
   const int nch = pre > 0 ? (pre + c.chunk - 1) / c.chunk : 0;
   WaveAcc<D> acc;
   acc.init();
-  fold_states<D, kStates>(acc, c, row * c.max_parts, nt, row * c.max_chunks, on ? nt + nch : 0, g);
+  if (on) fold_partial<D>(acc, ml_t.x, ml_t.y, o_t, g);
+  fold_states<D, kStates>(acc, c, row * c.max_parts + 1, nt - 1, 0, on ? nt - 1 : 0, g);
+  if (on && nch > 0) fold_partial<D>(acc, ml_c.x, ml_c.y, o_c, g);
+  fold_states<D, kStates>(acc, c, 0, 0, row * c.max_chunks + 1, on ? nch - 1 : 0, g);
   const float L = column_sum(acc.l_run);
   if (!on) return;
   const float inv = p.v_scale / (L + 1e-6f);
