@@ -48,13 +48,7 @@ struct RacParams {
   float k_scale, v_scale;
   float k_inv, v_inv;
   int32_t scales_pow2;
-  // Set by launch_reshape_and_cache: the call writes at least
-  // kRacStreamBytes of cache, so runs of consecutive slots in the paged
-  // layouts are stored nontemporally (reshape_and_cache.hip).
-  int32_t stream_runs;
 };
-
-constexpr int64_t kRacStreamBytes = int64_t(8) << 20;
 
 hipError_t launch_reshape_and_cache(const RacParams& p, bool aligned, hipStream_t stream);
 

@@ -62,28 +62,7 @@ __device__ __forceinline__ uint4 load_vec16(const typename Elem<S>::storage* __r
   }
 }
 
-typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
-
 // ---- paged 5-D layout: one wavefront per (token, head) ------------------------
-// Store policy.  A token whose slot continues its neighbour's in the batch
-// (slot_mapping[i +- 1] == slot -+ 1: a run of consecutive slots, as a
-// prefill writes whole blocks) is stored with the nontemporal policy when
-// the call writes at least kRacStreamBytes of cache (RacParams::stream_runs):
-// a run fills whole cache lines, nothing in the launch reads them back, and
-// a large append's lines parked in L2 slow the decode that reads them next.
-// Measured on MI355X (radix-shared decode, B256, 32/8 heads, D128, bf16,
-// 10% of private blocks rewritten per step, ~7.5k tokens per append): the
-// first decode after the appends 88.3 -> 77.9 us per launch with every
-// store nontemporal.  Scattered tokens (one per block, as a decode step
-// appends) and small appends keep the default policy: nontemporal stores
-// measured 5% slower on 4096 random slots, and on 1024 consecutive slots
-// rewritten back to back 16.8 against 7.4 us (the default policy keeps that
-// small write set in the caches).
-__device__ __forceinline__ bool rac_in_run(const RacParams& p, int64_t tok, int32_t slot) {
-  return (tok + 1 < p.num_tokens && p.slot_mapping[tok + 1] == slot + 1) ||
-         (tok > 0 && p.slot_mapping[tok - 1] == slot - 1);
-}
-
 template <class KT, class CT, bool ALIGNED>
 __global__ __launch_bounds__(256) void rac_paged5d_kernel(RacParams p) {
   using KS = typename Elem<KT>::storage;
@@ -105,14 +84,6 @@ __global__ __launch_bounds__(256) void rac_paged5d_kernel(RacParams p) {
   CS* kdst = static_cast<CS*>(p.key_cache) + region;    // [D/X][bs][X]
   CS* vdst = static_cast<CS*>(p.value_cache) + region;  // [D][bs]
   const int nchunk = D / X;
-  if (ALIGNED && p.stream_runs && rac_in_run(p, tok, slot)) {
-    for (int c = lane; c < nchunk; c += 64)
-      __builtin_nontemporal_store(__builtin_bit_cast(u32x4_t, load_vec16<KT, CT>(ksrc + c * X)),
-                                  reinterpret_cast<u32x4_t*>(kdst + ((int64_t)c * p.block_size + off) * X));
-    for (int d = lane; d < D; d += 64)
-      __builtin_nontemporal_store(convert_elem<KT, CT>(vsrc[d]), vdst + (int64_t)d * p.block_size + off);
-    return;
-  }
   for (int c = lane; c < nchunk; c += 64)
     convert_run<KT, CT, X, ALIGNED>(ksrc + c * X, kdst + ((int64_t)c * p.block_size + off) * X);
   for (int d = lane; d < D; d += 64)
@@ -153,6 +124,7 @@ __global__ __launch_bounds__(256) void rac_token_major_kernel(RacParams p) {
 // if-statement instead measured ~15% slower at the same instruction count.)
 // The source rows are loaded with the nontemporal policy when no conversion
 // is needed: each is read once.
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
 // Measured at 4096 tokens x 8 heads x D 128, bf16, 65,536 slots (median of
 // interleaved runs, one process per variant): one token per wavefront, four
@@ -295,25 +267,13 @@ __global__ __launch_bounds__(256) void rac_fp8_paged5d_kernel(RacParams p) {
   const int64_t region = ((int64_t)blk * p.num_heads + head) * (int64_t)D * p.block_size;
   uint8_t* kdst = static_cast<uint8_t*>(p.key_cache) + region;    // [D/16][bs][16]
   uint8_t* vdst = static_cast<uint8_t*>(p.value_cache) + region;  // [D][bs]
-  // Store policy as in rac_paged5d_kernel.
-  const bool nt = p.stream_runs && rac_in_run(p, tok, slot);
   for (int c = lane; c < D / 8; c += 64) {  // 8-element halves of the 16-byte chunks
     const uint2 k = encode8<KT>(ksrc + 8 * c, p.k_scale, p.k_inv, pow2);
-    uint32_t* kd = reinterpret_cast<uint32_t*>(kdst + ((int64_t)(c >> 1) * p.block_size + off) * 16 + (c & 1) * 8);
-    if (nt) {
-      __builtin_nontemporal_store(k.x, kd);
-      __builtin_nontemporal_store(k.y, kd + 1);
-    } else {
-      *reinterpret_cast<uint2*>(kd) = k;
-    }
+    *reinterpret_cast<uint2*>(kdst + ((int64_t)(c >> 1) * p.block_size + off) * 16 + (c & 1) * 8) = k;
   }
-  for (int d = lane; d < D; d += 64) {
-    const uint8_t v = (uint8_t)fp8_e4m3_encode(fp8_scaled(to_f32<KT>(vsrc[d]), p.v_scale, p.v_inv, pow2));
-    if (nt)
-      __builtin_nontemporal_store(v, vdst + (int64_t)d * p.block_size + off);
-    else
-      vdst[(int64_t)d * p.block_size + off] = v;
-  }
+  for (int d = lane; d < D; d += 64)
+    vdst[(int64_t)d * p.block_size + off] =
+        (uint8_t)fp8_e4m3_encode(fp8_scaled(to_f32<KT>(vsrc[d]), p.v_scale, p.v_inv, pow2));
 }
 
 template <class KT>
@@ -365,11 +325,8 @@ static hipError_t launch_rac_typed(const RacParams& p, bool aligned, hipStream_t
   return hipGetLastError();
 }
 
-hipError_t launch_reshape_and_cache(const RacParams& params, bool aligned, hipStream_t stream) {
-  if (params.num_tokens == 0) return hipSuccess;
-  RacParams p = params;
-  const int64_t cache_bytes = int64_t(p.cache_dtype == kF32 ? 4 : p.cache_dtype == kFP8 ? 1 : 2) * 2 * p.num_tokens * p.num_heads * p.head_size;
-  p.stream_runs = cache_bytes >= kRacStreamBytes;
+hipError_t launch_reshape_and_cache(const RacParams& p, bool aligned, hipStream_t stream) {
+  if (p.num_tokens == 0) return hipSuccess;
   const int kt = p.kv_dtype, ct = p.cache_dtype;
   if (kt == kF32 && ct == kF32) return launch_rac_typed<F32, F32>(p, aligned, stream);
   if (kt == kF16 && ct == kF16) return launch_rac_typed<F16, F16>(p, aligned, stream);

@@ -60,8 +60,8 @@ def test_paged5d(kv_dtype, bs, scales):
 
 @pytest.mark.parametrize("kv_dtype", ["float32", "bfloat16"])
 def test_paged5d_large_append_of_slot_runs(kv_dtype):
-    # 4096 tokens x 8 heads x D 128: 8 MiB of codes written, the size from
-    # which tokens inside runs of consecutive slots are stored nontemporally.
+    # 4096 tokens x 8 heads x D 128 whose slots come in runs: single-byte V
+    # codes of neighbouring tokens land in the same 16-byte rows.
     H, D, nb, bs = 8, 128, 1024, 16
     rng = np.random.default_rng(77)
     slots = run_slots(rng, 4096, nb, bs)

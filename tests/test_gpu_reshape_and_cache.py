@@ -5,8 +5,8 @@ Cases: the reference test's fixture geometry and shape sweep
 (kv dtype -> cache dtype) pair of reshape_and_cache.metal:91-95 in both
 layouts, strided and misaligned sources, padding-only and empty batches,
 the 4096-token append workload at full size (65,536 slots, 5% padding), and
-appends large enough (at least 8 MiB of cache written) that their runs of
-consecutive slots take the nontemporal store path.
+large appends whose slots come in runs of consecutive slots (whole and
+partial blocks, as a prefill writes them) mixed with scattered slots.
 Caches start from random bits so untouched slots are checked too.
 """
 
@@ -216,10 +216,10 @@ def test_append_workload_full_size(layout):
 @pytest.mark.parametrize("kv_dtype,cache_dtype", [("bfloat16", "bfloat16"), ("float16", "float16"),
                                                   ("float32", "float32"), ("float32", "bfloat16")])
 def test_large_append_of_slot_runs(kv_dtype, cache_dtype):
-    # 4096 tokens x 8 heads x D 128: 16 MiB (32 MiB for float32 caches) of
-    # cache written, above the 8 MiB from which tokens inside runs of
-    # consecutive slots are stored nontemporally; scattered tokens and
-    # padding in the same launch take the default stores.
+    # 4096 tokens x 8 heads x D 128 (16 MiB of cache written, 32 MiB for
+    # float32 caches): neighbouring tokens write neighbouring bytes of the
+    # same V rows and K chunks, so the stores of different wavefronts meet in
+    # the same cache lines.
     case = make_run_append_case(31, N=4096, H=8, D=128, num_blocks=1024, block_size=16,
                                 kv_dtype=kv_dtype, cache_dtype=cache_dtype)
     s = case.slot_mapping
