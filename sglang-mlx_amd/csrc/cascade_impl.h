@@ -793,45 +793,50 @@ __global__ __launch_bounds__(64) void paged_cascade_merge_kernel(DecodeParams p,
   bool on = row0 < (int64_t)p.num_seqs * p.num_heads;
   const int64_t row = on ? row0 : 0;
   const int seq = (int)(row / p.num_heads);
-  // The row's first tail-partition state and first prefix-chunk state are
-  // loaded together with its context and prefix lengths, in one round trip
-  // instead of three: both slots exist for every row, and each is folded
-  // below only if the row has it (a slot this call did not write may hold
-  // inf or NaN).  The fold order is unchanged: tail partitions, then chunks.
+  // The row's first tail-partition state and its first kEarly prefix-chunk
+  // states are loaded together with its context and prefix lengths, in one
+  // round trip: those slots exist for every row (chunk slots past the
+  // workspace's max_chunks are replaced by slot 0 and never used), and each
+  // is folded below only if the row has it (a slot this call did not write
+  // may hold inf or NaN).  The fold order is unchanged: tail partitions,
+  // then chunks.  (A 2048-token prefix in 512-token chunks, as the plan
+  // picks to fill the CUs, gives a row 4 chunk states and 1 tail state.)
+  constexpr int kEarly = 4;
   const uint32_t ctx = (uint32_t)p.context_lens[seq];
   const int plan_len = c.prefix_lens[seq];
-  const float2 ml_t = *reinterpret_cast<const float2*>(c.ws_tail_ml + row * c.max_parts * 2);
-  const float2 ml_c = *reinterpret_cast<const float2*>(c.ws_ml + row * c.max_chunks * 2);
-  float4 o_t[DT], o_c[DT];
+  float2 ml_e[1 + kEarly];
+  float4 o_e[1 + kEarly][DT];
   {
-    const float* wt = c.ws_tail_o + row * c.max_parts * D + 4 * g;
-    const float* wc = c.ws_o + row * c.max_chunks * D + 4 * g;
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
-      o_t[dt] = *reinterpret_cast<const float4*>(wt + 16 * dt);
-      o_c[dt] = *reinterpret_cast<const float4*>(wc + 16 * dt);
+    for (int e = 0; e <= kEarly; ++e) {
+      const float* wml = e == 0 ? c.ws_tail_ml + row * c.max_parts * 2
+                                : c.ws_ml + (row * c.max_chunks + (e - 1 < c.max_chunks ? e - 1 : 0)) * 2;
+      const float* wo = e == 0 ? c.ws_tail_o + row * c.max_parts * D
+                               : c.ws_o + (row * c.max_chunks + (e - 1 < c.max_chunks ? e - 1 : 0)) * D;
+      ml_e[e] = *reinterpret_cast<const float2*>(wml);
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) o_e[e][dt] = *reinterpret_cast<const float4*>(wo + 4 * g + 16 * dt);
     }
-    // The asm takes every one of those values, so all the loads are issued
-    // before it; without it the compiler moves the state loads past the
-    // branches on the lengths.
-    float anchor = ml_t.x + ml_t.y + ml_c.x + ml_c.y;
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) anchor += o_t[dt].x + o_t[dt].y + o_t[dt].z + o_t[dt].w + o_c[dt].x + o_c[dt].y +
-                                              o_c[dt].z + o_c[dt].w;
-    asm volatile("" ::"v"(anchor), "v"(ctx), "v"(plan_len));
+    // No load may move past this asm (it may write memory), so all of them
+    // are issued before the branches on the lengths; without it the
+    // compiler moves the state loads into those branches.  It uses no
+    // value, so nothing waits here.
+    asm volatile("" ::: "memory");
   }
   const bool live = ctx != 0 && ctx <= (uint32_t)p.max_seq_len;
   const int pre = usable_prefix_of<BS>(c, plan_len, live);
   const int np = tail_parts(c, live ? (int)ctx - min(pre, (int)ctx) : 0);
   on = on && !(pre == 0 && np == 1);  // rows the tail role wrote
   const int nt = min(np, c.max_parts);  // >= 1
-  const int nch = pre > 0 ? (pre + c.chunk - 1) / c.chunk : 0;
+  const int nch = pre > 0 ? (pre + c.chunk - 1) / c.chunk : 0;  // <= max_chunks
   WaveAcc<D> acc;
   acc.init();
-  if (on) fold_partial<D>(acc, ml_t.x, ml_t.y, o_t, g);
+  if (on) fold_partial<D>(acc, ml_e[0].x, ml_e[0].y, o_e[0], g);
   fold_states<D, kStates>(acc, c, row * c.max_parts + 1, nt - 1, 0, on ? nt - 1 : 0, g);
-  if (on && nch > 0) fold_partial<D>(acc, ml_c.x, ml_c.y, o_c, g);
-  fold_states<D, kStates>(acc, c, 0, 0, row * c.max_chunks + 1, on ? nch - 1 : 0, g);
+#pragma unroll
+  for (int e = 1; e <= kEarly; ++e)
+    if (on && e - 1 < nch) fold_partial<D>(acc, ml_e[e].x, ml_e[e].y, o_e[e], g);
+  fold_states<D, kStates>(acc, c, 0, 0, row * c.max_chunks + kEarly, on ? nch - kEarly : 0, g);
   const float L = column_sum(acc.l_run);
   if (!on) return;
   const float inv = p.v_scale / (L + 1e-6f);
