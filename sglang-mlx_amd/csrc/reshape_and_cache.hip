@@ -62,6 +62,61 @@ __device__ __forceinline__ uint4 load_vec16(const typename Elem<S>::storage* __r
   }
 }
 
+// ---- paged 5-D layout, whole-block runs ------------------------------------------
+// When bs consecutive batch tokens write slots blk*bs .. blk*bs + bs - 1 in
+// order (a prefill writing whole blocks), the (block, head) region's K
+// ([D/8][bs][8]) and V ([D][bs]) are each one contiguous run of D*bs
+// elements that these tokens fill completely.  The wavefront of the run's
+// token at offset `off` then writes slice `off` of each region -- its
+// 16-byte units off*D/8 .. off*D/8 + D/8 - 1, gathered from the run's
+// source rows -- so every unit is written once, whole, and the bs
+// wavefronts of a run cover the region.  K unit u holds dimensions 8c ..
+// 8c+7 of token t (u = c*bs + t); V unit u holds tokens 8g .. 8g+7 of
+// dimension d (u = d*bs/8 + g).  The per-token path instead writes a
+// token's V as single 2-byte elements 2*bs bytes apart, each a partial
+// write of its line.  2-byte cache types (the kernel's ALIGNED case).
+template <class KT, class CT, int BS>
+__device__ __forceinline__ void rac_run_slice(const RacParams& p, int64_t first, int off, int head, int64_t blk,
+                                              int lane) {
+  using KS = typename Elem<KT>::storage;
+  using CS = typename Elem<CT>::storage;
+  static_assert(Elem<CT>::kBytes == 2 && BS % 8 == 0, "16-byte units of 2-byte elements");
+  constexpr int X = 8;
+  const int D = p.head_size;
+  const int per = D / X;  // units per wavefront and region (<= 32)
+  if (lane >= 2 * per) return;
+  const int64_t region = (blk * p.num_heads + head) * (int64_t)D * BS;
+  const int64_t hoff = (int64_t)head * D;
+  const bool is_v = lane >= per;
+  const int u = off * per + (is_v ? lane - per : lane);
+  if (!is_v) {
+    const int c = u / BS, t = u % BS;
+    const KS* src = static_cast<const KS*>(p.key) + (first + t) * p.key_stride + hoff + c * X;
+    *reinterpret_cast<uint4*>(static_cast<CS*>(p.key_cache) + region + (int64_t)u * X) = load_vec16<KT, CT>(src);
+  } else {
+    const int d = u / (BS / 8), g = u % (BS / 8);
+    const KS* src = static_cast<const KS*>(p.value) + (first + 8 * g) * p.value_stride + hoff + d;
+    CS e[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) e[j] = convert_elem<KT, CT>(src[j * p.value_stride]);
+    *reinterpret_cast<uint4*>(static_cast<CS*>(p.value_cache) + region + (int64_t)u * X) =
+        make_uint4(pack2(e[0], e[1]), pack2(e[2], e[3]), pack2(e[4], e[5]), pack2(e[6], e[7]));
+  }
+}
+
+// True when the token at batch position tok (slot `slot`, offset `off` in
+// its block) lies in a whole-block run: positions tok - off .. tok - off +
+// bs - 1 hold slots slot - off .. slot - off + bs - 1.  Wave-uniform; lanes
+// 0 .. bs-1 each check one entry.
+__device__ __forceinline__ bool rac_whole_block(const RacParams& p, int64_t tok, int32_t slot, int off, int lane) {
+  const int bs = p.block_size;
+  const int64_t first = tok - off;
+  if (first < 0 || first + bs > p.num_tokens) return false;
+  bool ok = true;
+  if (lane < bs) ok = p.slot_mapping[first + lane] == slot - off + lane;
+  return __all(ok);
+}
+
 // ---- paged 5-D layout: one wavefront per (token, head) ------------------------
 template <class KT, class CT, bool ALIGNED>
 __global__ __launch_bounds__(256) void rac_paged5d_kernel(RacParams p) {
@@ -77,6 +132,18 @@ __global__ __launch_bounds__(256) void rac_paged5d_kernel(RacParams p) {
   if (slot < 0 || (int64_t)slot >= p.num_slots) return;
   const int64_t blk = slot / p.block_size;
   const int off = slot - (int)blk * p.block_size;
+  if constexpr (ALIGNED && Elem<CT>::kBytes == 2) {
+    const int bs = p.block_size;
+    // (Head sizes that are multiples of 8, at most 256: D/8 units per
+    // wavefront and region, K and V units on separate lanes.)
+    if ((bs == 8 || bs == 16 || bs == 32) && p.head_size % 8 == 0 && p.head_size <= 256 &&
+        rac_whole_block(p, tok, slot, off, lane)) {
+      if (bs == 8) rac_run_slice<KT, CT, 8>(p, tok - off, off, head, blk, lane);
+      else if (bs == 16) rac_run_slice<KT, CT, 16>(p, tok - off, off, head, blk, lane);
+      else rac_run_slice<KT, CT, 32>(p, tok - off, off, head, blk, lane);
+      return;
+    }
+  }
   const int D = p.head_size;
   const KS* ksrc = static_cast<const KS*>(p.key) + tok * p.key_stride + (int64_t)head * D;
   const KS* vsrc = static_cast<const KS*>(p.value) + tok * p.value_stride + (int64_t)head * D;

@@ -10,6 +10,8 @@ partial blocks, as a prefill writes them) mixed with scattered slots.
 Caches start from random bits so untouched slots are checked too.
 """
 
+import dataclasses
+
 import numpy as np
 import pytest
 import torch
@@ -226,3 +228,31 @@ def test_large_append_of_slot_runs(kv_dtype, cache_dtype):
     in_run = (s[1:] == s[:-1] + 1) & (s[:-1] >= 0)
     assert in_run.mean() > 0.5 and (~in_run).sum() > 100
     check_paged5d(case, 1024, 8, 128)
+
+
+@pytest.mark.parametrize("block_size", [8, 16, 32])
+@pytest.mark.parametrize("kv_dtype,cache_dtype", [("bfloat16", "bfloat16"), ("float32", "float16")])
+@pytest.mark.parametrize("head_dim", [64, 128, 256])
+def test_whole_block_runs(block_size, kv_dtype, cache_dtype, head_dim):
+    # Whole blocks written by consecutive tokens take the one-wavefront-per-
+    # (block, head) path; partial blocks, single slots and padding in the
+    # same batch take the per-token path.
+    H = 4
+    case = make_run_append_case(40 + block_size, N=600, H=H, D=head_dim, num_blocks=160, block_size=block_size,
+                                kv_dtype=kv_dtype, cache_dtype=cache_dtype)
+    s = case.slot_mapping
+    whole = sum(1 for i in range(0, len(s) - block_size + 1)
+                if s[i] >= 0 and s[i] % block_size == 0
+                and all(s[i + k] == s[i] + k for k in range(block_size)))
+    assert whole >= 5
+    check_paged5d(case, 160, H, head_dim)
+
+
+@pytest.mark.parametrize("start", [0, 5, 16])
+@pytest.mark.parametrize("N", [1, 15, 16, 17, 300, 1024])
+def test_consecutive_slots(start, N):
+    # The reference benchmark's slot mapping (slots start .. start+N-1, as a
+    # prefill writes): whole blocks in the middle, partial blocks at the ends.
+    case = make_append_case(N + start, N=N, H=8, D=128, num_slots=128 * 16, block_size=16, pad_frac=0.0)
+    case = dataclasses.replace(case, slot_mapping=np.arange(start, start + N, dtype=np.int32))
+    check_paged5d(case, 128, 8, 128)
