@@ -67,14 +67,15 @@ __device__ __forceinline__ uint4 load_vec16(const typename Elem<S>::storage* __r
 // order (a prefill writing whole blocks), the (block, head) region's K
 // ([D/8][bs][8]) and V ([D][bs]) are each one contiguous run of D*bs
 // elements that these tokens fill completely.  The wavefront of the run's
-// token at offset `off` then writes slice `off` of each region -- its
-// 16-byte units off*D/8 .. off*D/8 + D/8 - 1, gathered from the run's
-// source rows -- so every unit is written once, whole, and the bs
-// wavefronts of a run cover the region.  K unit u holds dimensions 8c ..
-// 8c+7 of token t (u = c*bs + t); V unit u holds tokens 8g .. 8g+7 of
-// dimension d (u = d*bs/8 + g).  The per-token path instead writes a
-// token's V as single 2-byte elements 2*bs bytes apart, each a partial
-// write of its line.  2-byte cache types (the kernel's ALIGNED case).
+// token at offset `off` then writes slice `off` of each region: elements
+// off*D .. off*D + D - 1, i.e. 16-byte units off*D/8 .. off*D/8 + D/8 - 1,
+// gathered from the run's source rows.  Every unit is written once and
+// whole, and the bs wavefronts of a run cover the region.  K unit u holds
+// dimensions 8c .. 8c+7 of token t (u = c*bs + t); V unit u holds tokens
+// 8g .. 8g+7 of dimension d (u = d*bs/8 + g).  The per-token path instead
+// writes a token's V as single 2-byte elements 2*bs bytes apart, each a
+// partial write of its line.  2-byte cache types (the kernel's ALIGNED
+// case).
 template <class KT, class CT, int BS>
 __device__ __forceinline__ void rac_run_slice(const RacParams& p, int64_t first, int off, int head, int64_t blk,
                                               int lane) {
@@ -83,24 +84,25 @@ __device__ __forceinline__ void rac_run_slice(const RacParams& p, int64_t first,
   static_assert(Elem<CT>::kBytes == 2 && BS % 8 == 0, "16-byte units of 2-byte elements");
   constexpr int X = 8;
   const int D = p.head_size;
-  const int per = D / X;  // units per wavefront and region (<= 32)
-  if (lane >= 2 * per) return;
-  const int64_t region = (blk * p.num_heads + head) * (int64_t)D * BS;
+  const int per = D / X;  // units per wavefront and region
+  const int64_t slice = (blk * p.num_heads + head) * (int64_t)D * BS + (int64_t)off * per * X;
   const int64_t hoff = (int64_t)head * D;
-  const bool is_v = lane >= per;
-  const int u = off * per + (is_v ? lane - per : lane);
-  if (!is_v) {
+  const KS* key = static_cast<const KS*>(p.key);
+  const KS* val = static_cast<const KS*>(p.value);
+  // Each lane moves two neighbouring elements of the slice: one store
+  // instruction writes 256 contiguous bytes of each region.
+  for (int i = 2 * lane; i < D; i += 128) {
+    const int u = off * per + i / X, e = i % X;
+    // K: dimensions 8c + e, +1 of token t.
     const int c = u / BS, t = u % BS;
-    const KS* src = static_cast<const KS*>(p.key) + (first + t) * p.key_stride + hoff + c * X;
-    *reinterpret_cast<uint4*>(static_cast<CS*>(p.key_cache) + region + (int64_t)u * X) = load_vec16<KT, CT>(src);
-  } else {
-    const int d = u / (BS / 8), g = u % (BS / 8);
-    const KS* src = static_cast<const KS*>(p.value) + (first + 8 * g) * p.value_stride + hoff + d;
-    CS e[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) e[j] = convert_elem<KT, CT>(src[j * p.value_stride]);
-    *reinterpret_cast<uint4*>(static_cast<CS*>(p.value_cache) + region + (int64_t)u * X) =
-        make_uint4(pack2(e[0], e[1]), pack2(e[2], e[3]), pack2(e[4], e[5]), pack2(e[6], e[7]));
+    const KS* ks = key + (first + t) * p.key_stride + hoff + X * c + e;
+    // V: tokens 8g + e, +1 of dimension d.
+    const int d = u / (BS / X), g = u % (BS / X);
+    const KS* vs = val + (first + X * g + e) * p.value_stride + hoff + d;
+    const uint32_t kw = pack2(convert_elem<KT, CT>(ks[0]), convert_elem<KT, CT>(ks[1]));
+    const uint32_t vw = pack2(convert_elem<KT, CT>(vs[0]), convert_elem<KT, CT>(vs[p.value_stride]));
+    *reinterpret_cast<uint32_t*>(static_cast<CS*>(p.key_cache) + slice + i) = kw;
+    *reinterpret_cast<uint32_t*>(static_cast<CS*>(p.value_cache) + slice + i) = vw;
   }
 }
 
@@ -134,10 +136,8 @@ __global__ __launch_bounds__(256) void rac_paged5d_kernel(RacParams p) {
   const int off = slot - (int)blk * p.block_size;
   if constexpr (ALIGNED && Elem<CT>::kBytes == 2) {
     const int bs = p.block_size;
-    // (Head sizes that are multiples of 8, at most 256: D/8 units per
-    // wavefront and region, K and V units on separate lanes.)
-    if ((bs == 8 || bs == 16 || bs == 32) && p.head_size % 8 == 0 && p.head_size <= 256 &&
-        rac_whole_block(p, tok, slot, off, lane)) {
+    // (Head sizes that are multiples of 8: whole 16-byte units per slice.)
+    if ((bs == 8 || bs == 16 || bs == 32) && p.head_size % 8 == 0 && rac_whole_block(p, tok, slot, off, lane)) {
       if (bs == 8) rac_run_slice<KT, CT, 8>(p, tok - off, off, head, blk, lane);
       else if (bs == 16) rac_run_slice<KT, CT, 16>(p, tok - off, off, head, blk, lane);
       else rac_run_slice<KT, CT, 32>(p, tok - off, off, head, blk, lane);
@@ -315,6 +315,43 @@ __global__ __launch_bounds__(256) void rac_fp8_token_major_kernel(RacParams p) {
   }
 }
 
+// Whole-block runs over FP8 caches (block sizes 16 and 32): as
+// rac_run_slice, with 16-byte units of 16 codes -- K unit u = c*bs + t
+// (dimensions 16c .. 16c+15 of token t), V unit u = d*bs/16 + g (tokens
+// 16g .. 16g+15 of dimension d); D/16 units (D bytes) per wavefront and
+// region.  Each lane encodes two neighbouring codes of the slice, so one
+// store instruction writes D/64 x 128 contiguous bytes and the encodes
+// spread over the whole wavefront.
+template <class KT, int BS>
+__device__ __forceinline__ void rac_fp8_run_slice(const RacParams& p, int64_t first, int off, int head, int64_t blk,
+                                                  int lane) {
+  using KS = typename Elem<KT>::storage;
+  static_assert(BS % 16 == 0, "16-byte units of 16 codes");
+  const int D = p.head_size;
+  const int per = D / 16;
+  const bool pow2 = p.scales_pow2 != 0;
+  const int64_t region = (blk * p.num_heads + head) * (int64_t)D * BS;
+  const int64_t slice = region + (int64_t)off * per * 16;
+  const int64_t hoff = (int64_t)head * D;
+  const KS* key = static_cast<const KS*>(p.key);
+  const KS* val = static_cast<const KS*>(p.value);
+  for (int i = 2 * lane; i < D; i += 128) {
+    const int u = off * per + i / 16, b = i % 16;
+    // K: dimensions 16c + b, +1 of token t.
+    const int c = u / BS, t = u % BS;
+    const KS* ks = key + (first + t) * p.key_stride + hoff + 16 * c + b;
+    const uint32_t k0 = fp8_e4m3_encode(fp8_scaled(to_f32<KT>(ks[0]), p.k_scale, p.k_inv, pow2));
+    const uint32_t k1 = fp8_e4m3_encode(fp8_scaled(to_f32<KT>(ks[1]), p.k_scale, p.k_inv, pow2));
+    // V: tokens 16g + b, +1 of dimension d.
+    const int d = u / (BS / 16), g = u % (BS / 16);
+    const KS* vs = val + (first + 16 * g + b) * p.value_stride + hoff + d;
+    const uint32_t v0 = fp8_e4m3_encode(fp8_scaled(to_f32<KT>(vs[0]), p.v_scale, p.v_inv, pow2));
+    const uint32_t v1 = fp8_e4m3_encode(fp8_scaled(to_f32<KT>(vs[p.value_stride]), p.v_scale, p.v_inv, pow2));
+    *reinterpret_cast<uint16_t*>(static_cast<uint8_t*>(p.key_cache) + slice + i) = (uint16_t)(k0 | (k1 << 8));
+    *reinterpret_cast<uint16_t*>(static_cast<uint8_t*>(p.value_cache) + slice + i) = (uint16_t)(v0 | (v1 << 8));
+  }
+}
+
 template <class KT>
 __global__ __launch_bounds__(256) void rac_fp8_paged5d_kernel(RacParams p) {
   using KS = typename Elem<KT>::storage;
@@ -328,6 +365,11 @@ __global__ __launch_bounds__(256) void rac_fp8_paged5d_kernel(RacParams p) {
   const int64_t blk = slot / p.block_size;
   const int off = slot - (int)blk * p.block_size;
   const int D = p.head_size;  // a multiple of 16
+  if ((p.block_size == 16 || p.block_size == 32) && rac_whole_block(p, tok, slot, off, lane)) {
+    if (p.block_size == 16) rac_fp8_run_slice<KT, 16>(p, tok - off, off, head, blk, lane);
+    else rac_fp8_run_slice<KT, 32>(p, tok - off, off, head, blk, lane);
+    return;
+  }
   const bool pow2 = p.scales_pow2 != 0;
   const KS* ksrc = static_cast<const KS*>(p.key) + tok * p.key_stride + (int64_t)head * D;
   const KS* vsrc = static_cast<const KS*>(p.value) + tok * p.value_stride + (int64_t)head * D;

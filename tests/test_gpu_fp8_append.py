@@ -59,11 +59,14 @@ def test_paged5d(kv_dtype, bs, scales):
 
 
 @pytest.mark.parametrize("kv_dtype", ["float32", "bfloat16"])
-def test_paged5d_large_append_of_slot_runs(kv_dtype):
-    # 4096 tokens x 8 heads x D 128 whose slots come in runs: single-byte V
-    # codes of neighbouring tokens land in the same 16-byte rows.
-    H, D, nb, bs = 8, 128, 1024, 16
-    rng = np.random.default_rng(77)
+@pytest.mark.parametrize("bs", [16, 32])
+def test_paged5d_large_append_of_slot_runs(kv_dtype, bs):
+    # 4096 tokens x 8 heads x D 128 whose slots come in runs: whole blocks
+    # are written as 16-byte units of 16 codes gathered over the run's
+    # tokens, the rest per token; the whole cache is compared.
+    H, D = 8, 128
+    nb = 1024 if bs == 16 else 600
+    rng = np.random.default_rng(77 + bs)
     slots = run_slots(rng, 4096, nb, bs)
     key, value = wide_values(rng, (4096, H, D), kv_dtype), wide_values(rng, (4096, H, D), kv_dtype)
     kc0 = rng.integers(0, 256, size=(nb, H, D // 16, bs, 16), dtype=np.uint8)
@@ -124,3 +127,23 @@ def test_rejections():
     with pytest.raises(ValueError, match="16-byte aligned"):
         kb = torch.zeros((4 * 8 * 128 + 8,), dtype=torch.bfloat16, device="cuda")[4:4 + 4 * 8 * 128].view(4, 8, 128)
         kernels.reshape_and_cache(kb, kb, kc, kc.clone(), s)
+
+
+@pytest.mark.parametrize("start", [0, 7])
+@pytest.mark.parametrize("D", [64, 128, 256])
+def test_paged5d_consecutive_slots(start, D):
+    # Slots start .. start+N-1, as a prefill writes them: whole blocks in the
+    # middle, partial blocks at the ends.
+    H, nb, bs, N = 4, 64, 16, 700
+    rng = np.random.default_rng(D + start)
+    key, value = wide_values(rng, (N, H, D), "bfloat16"), wide_values(rng, (N, H, D), "bfloat16")
+    slots = np.arange(start, start + N, dtype=np.int32)
+    kc0 = rng.integers(0, 256, size=(nb, H, D // 16, bs, 16), dtype=np.uint8)
+    vc0 = rng.integers(0, 256, size=(nb, H, D, bs), dtype=np.uint8)
+    kc, vc = to_torch(kc0, FP8), to_torch(vc0, FP8)
+    kernels.reshape_and_cache(to_torch(key, "bfloat16"), to_torch(value, "bfloat16"), kc, vc, to_index(slots),
+                              k_scale=0.5, v_scale=4.0)
+    torch.cuda.synchronize()
+    rk, rv = orc.reshape_and_cache_paged5d(key, value, kc0, vc0, slots, "bfloat16", FP8, 0.5, 4.0)
+    np.testing.assert_array_equal(to_numpy(kc), rk)
+    np.testing.assert_array_equal(to_numpy(vc), rv)
