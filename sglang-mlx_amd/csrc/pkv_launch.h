@@ -48,7 +48,13 @@ struct RacParams {
   float k_scale, v_scale;
   float k_inv, v_inv;
   int32_t scales_pow2;
+  // Set by launch_reshape_and_cache: the call writes at least
+  // kRacStreamKBytes of K, so the paged layout's per-token K stores are
+  // nontemporal (reshape_and_cache.hip).
+  int32_t stream_k;
 };
+
+constexpr int64_t kRacStreamKBytes = int64_t(4) << 20;
 
 hipError_t launch_reshape_and_cache(const RacParams& p, bool aligned, hipStream_t stream);
 
