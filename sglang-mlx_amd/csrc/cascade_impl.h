@@ -16,14 +16,16 @@
 //     tile's query rows (members x GQA heads, up to 128; each wavefront 32
 //     rows as two 16-column MFMA query sets held in registers) against one
 //     chunk of the group's prefix.  The chunk's K and V are staged through
-//     LDS two tiles of 16 tokens at a time (three buffers, two stages in
-//     flight) by direct-to-LDS buffer loads, in the order the MFMA operands
-//     want; every K/V byte is read from HBM (or L2) once per workgroup and
-//     from LDS once per wavefront, and feeds 32 query rows there.  FP8 codes
-//     are dequantised as they leave LDS.  Scores S^T = K Q^T and O^T += V^T P^T
-//     on v_mfma_f32_16x16x32 over tile pairs, online softmax in the log2
-//     domain; each row's partial state (max, sum, unnormalised output) goes
-//     to the workspace slot of its (sequence, head, chunk).
+//     LDS two tiles of 16 tokens at a time (16-bit caches: four buffers,
+//     the scores of the next pair computed while the current pair's
+//     softmax runs) by direct-to-LDS buffer loads, in the order the MFMA
+//     operands want; every K/V byte is read from HBM (or L2) once per
+//     workgroup and from LDS once per wavefront, and feeds 32 query rows
+//     there.  FP8 codes are dequantised once per stage into a 16-bit LDS
+//     image.  Scores S^T = K Q^T and O^T += V^T P^T on v_mfma_f32_16x16x32
+//     over tile pairs, online softmax in the log2 domain; each row's
+//     partial state (max, sum, unnormalised output) goes to the workspace
+//     slot of its (sequence, head, chunk).
 //   * Tail role (the rest): one wavefront per (tail partition, KV head)
 //     item, longest partition first: the partition's tokens (after the
 //     sequence's prefix) through the one-sequence tile pipeline.  A
@@ -50,11 +52,11 @@ constexpr int kCascadeWaves = 4;                               // wavefronts per
 constexpr int kPrefixSets = 2;                                 // 16-column query sets per wavefront
 constexpr int kPrefixRows = kCascadeWaves * kPrefixSets * 16;  // query rows per prefix workgroup
 constexpr int kPrefixStageTiles = 2;                           // 16-token tiles per LDS stage (one pair)
-// LDS stage buffers (NB - 1 stages in flight).  Four (three stages ahead)
-// timed the same for the prefix pass alone (35.7 against 35.6 us on the
-// radix-shared B256 workload) and cost the FP8 cascade 2.7 us (LDS 67.6
-// instead of 51 KB per workgroup).
-constexpr int kPrefixBuffers = 3;
+// LDS stage buffers of 16-bit caches: four, so that a step can read the
+// next stage's K for its look-ahead scores while two later stages load
+// (67.6 KB of LDS per workgroup, two workgroups per CU).  FP8 caches stage
+// through two code buffers and two 16-bit images instead.
+constexpr int kPrefixBuffers = 4;
 constexpr int kTailBuffers = 2;                                // tile buffers per tail wavefront
 
 // Largest block-table span of one prefix chunk (8-token blocks).
@@ -459,35 +461,15 @@ __device__ __forceinline__ void prefix_role(const DecodeParams& p, const Cascade
 #pragma unroll
   for (int s = 0; s < NS; ++s) acc[s].init();
 
-  // One tile pair: scores of both tiles per query set, one online-softmax
-  // step over their 32 tokens, P V^T on 16x16x32 MFMAs.  The scores of all
-  // sets are issued first, set by set; then each set's softmax step is
-  // followed by its PV product.  Set 0's softmax VALU work so runs while
-  // set 1's score MFMAs execute, and set 1's while set 0's PV MFMAs do
-  // (radix-shared B256: 70.1 -> 68.4 us per launch against running each
-  // phase for both sets before the next).
-  // img: the pair is a 16-bit image of an FP8 stage (MT's layout) rather
-  // than the stage as loaded.
-  auto consume_pair = [&](auto img, const uint4* ta, const uint4* tb, uint32_t live_a, uint32_t live_b,
-                          int tok_a) __attribute__((always_inline)) {
-    using OT = std::conditional_t<decltype(img)::value, MT, CT>;
-    PrefixOperands<OT, MT, D> op;
-    read_pair<OT, MT, D>(op, ta, tb, lane, g, col);
+  // The softmax step and PV product of one tile pair, given its scores (sa:
+  // tile A, sb: tile B, per query set) and its PV operands.  Per set: the
+  // softmax step, then its PV product, so that set s+1's softmax runs while
+  // set s's PV MFMAs execute.
+  auto softmax_pv = [&](const f32x4 (&sa)[NS], const f32x4 (&sb)[NS], const uint4 (&v)[DT], uint32_t live_a,
+                        uint32_t live_b, int tok_a) __attribute__((always_inline)) {
     const int va = tok_a + 4 * g, vb = va + kTile;
-    f32x4 sa[NS], sb[NS];
-#pragma unroll
-    for (int s = 0; s < NS; ++s) sa[s] = sb[s] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < NS; ++s)
-#pragma unroll
-      for (int j = 0; j < KSTEPS; ++j) {
-        sa[s] = Mma<MT>::k32(op.ka[j], qa[s][j], sa[s]);
-        sb[s] = Mma<MT>::k32(op.kb[j], qa[s][j], sb[s]);
-      }
     // Token liveness of the lane's 4 + 4 tokens; the context bound per set.
     const uint32_t la = (live_a >> (4 * g)) & 15u, lb = (live_b >> (4 * g)) & 15u;
-    // Per set: softmax step, then its PV product.  Set s+1's softmax runs
-    // while set s's PV MFMAs execute (and set 0's while set 1's scores do).
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
       float sc[8];
@@ -534,8 +516,36 @@ __device__ __forceinline__ void prefix_role(const DecodeParams& p, const Cascade
       const uint4 pp = make_uint4(pack_p<MT>(pr[0], pr[1]), pack_p<MT>(pr[2], pr[3]), pack_p<MT>(pr[4], pr[5]),
                                   pack_p<MT>(pr[6], pr[7]));
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) a.o[dt] = Mma<MT>::k32(op.v[dt], pp, a.o[dt]);
+      for (int dt = 0; dt < DT; ++dt) a.o[dt] = Mma<MT>::k32(v[dt], pp, a.o[dt]);
     }
+  };
+  auto scores_of = [&](const uint4 (&ka)[KSTEPS], const uint4 (&kb)[KSTEPS], f32x4 (&sa)[NS], f32x4 (&sb)[NS])
+                       __attribute__((always_inline)) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) sa[s] = sb[s] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+#pragma unroll
+      for (int j = 0; j < KSTEPS; ++j) {
+        sa[s] = Mma<MT>::k32(ka[j], qa[s][j], sa[s]);
+        sb[s] = Mma<MT>::k32(kb[j], qa[s][j], sb[s]);
+      }
+  };
+  // One tile pair as one step (the FP8 path): scores of both tiles per query
+  // set (all sets first, so that set 0's softmax runs while set 1's score
+  // MFMAs execute), then softmax_pv.  img: the pair is a 16-bit image of an
+  // FP8 stage (MT's layout) rather than the stage as loaded.  Measured on the
+  // radix-shared B256 workload (16-bit caches, one pair per step): 70.1 ->
+  // 68.4 us per launch against running each phase for both sets before the
+  // next; scores one stage ahead (below) then 68.3 -> 67.6 us.
+  auto consume_pair = [&](auto img, const uint4* ta, const uint4* tb, uint32_t live_a, uint32_t live_b,
+                          int tok_a) __attribute__((always_inline)) {
+    using OT = std::conditional_t<decltype(img)::value, MT, CT>;
+    PrefixOperands<OT, MT, D> op;
+    read_pair<OT, MT, D>(op, ta, tb, lane, g, col);
+    f32x4 sa[NS], sb[NS];
+    scores_of(op.ka, op.kb, sa, sb);
+    softmax_pv(sa, sb, op.v, live_a, live_b, tok_a);
   };
   // Direct-to-LDS loads a wavefront issues per stage; s_waitcnt immediates
   // (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt in 6:4 left at its
@@ -594,19 +604,58 @@ __device__ __forceinline__ void prefix_role(const DecodeParams& p, const Cascade
     }
   } else {
 
-  // Step k of a turn consumes stage st (buffer k), issues stage st + NB - 1
-  // into the buffer consumed one step earlier, waits for stage st + 1 (the
-  // stages after it may stay in flight) and meets the workgroup at a
-  // barrier.
+  // Scores one stage ahead.  Step st (buffer k) issues stage st + 3 into
+  // the buffer stage st - 1 used, reads stage st's V and stage st + 1's K,
+  // issues stage st + 1's score MFMAs and then runs stage st's softmax and
+  // PV product on the scores the previous step computed: the score MFMAs
+  // of one pair execute under the softmax VALU work of the one before.  It
+  // then waits for stage st + 2 (whose K the next step reads; stage st + 3
+  // may stay in flight) and meets the workgroup at a barrier.  The last
+  // step's look-ahead reads a buffer it never uses.
+  static_assert(NB == 4, "scores one stage ahead need four stage buffers");
+  auto read_k = [&](auto k, uint4 (&ka)[KSTEPS], uint4 (&kb)[KSTEPS]) __attribute__((always_inline)) {
+    const uint4* ta = buffer(k)[0];
+    const uint4* tb = buffer(k)[1];
+#pragma unroll
+    for (int j = 0; j < KSTEPS; ++j) {
+      ka[j] = ta[64 * j + lane];
+      kb[j] = tb[64 * j + lane];
+    }
+  };
+  auto read_v = [&](auto k, uint4 (&v)[DT]) __attribute__((always_inline)) {
+    const char* va = reinterpret_cast<const char*>(buffer(k)[0] + PT::kKUnits);
+    const char* vb = reinterpret_cast<const char*>(buffer(k)[1] + PT::kKUnits);
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const int o = (16 * dt + col) * 32 + 8 * g;
+      const uint2 x = *reinterpret_cast<const uint2*>(va + o), y = *reinterpret_cast<const uint2*>(vb + o);
+      v[dt] = make_uint4(x.x, x.y, y.x, y.y);
+    }
+  };
+  f32x4 sa[NS], sb[NS];
+  {
+    uint4 ka[KSTEPS], kb[KSTEPS];
+    read_k(I0{}, ka, kb);
+    scores_of(ka, kb, sa, sb);
+  }
   auto step = [&](auto k, int st) __attribute__((always_inline)) {
     constexpr int K = decltype(k)::value;
-    if (st + NB - 1 < nstages) stage(std::integral_constant<int, (K + NB - 1) % NB>{}, st + NB - 1);
-    consume_pair(std::false_type{}, buffer(k)[0], buffer(k)[1], s_live[K][0], s_live[K][1],
-                   t0 + st * ST * kTile);
-    const int later = min(NB - 2, nstages - 2 - st);  // stages issued after st + 1
-    if (later >= 2)
-      __builtin_amdgcn_s_waitcnt(kWait2);
-    else if (later == 1)
+    if (st + 3 < nstages) stage(std::integral_constant<int, (K + 3) % NB>{}, st + 3);
+    uint4 v[DT];
+    read_v(k, v);
+    f32x4 na[NS], nb[NS];
+    {
+      uint4 ka[KSTEPS], kb[KSTEPS];
+      read_k(std::integral_constant<int, (K + 1) % NB>{}, ka, kb);
+      scores_of(ka, kb, na, nb);
+    }
+    softmax_pv(sa, sb, v, s_live[K][0], s_live[K][1], t0 + st * ST * kTile);
+#pragma unroll
+    for (int s2 = 0; s2 < NS; ++s2) {
+      sa[s2] = na[s2];
+      sb[s2] = nb[s2];
+    }
+    if (st + 3 < nstages)
       __builtin_amdgcn_s_waitcnt(kWait1);
     else
       __builtin_amdgcn_s_waitcnt(kWait0);
@@ -618,12 +667,9 @@ __device__ __forceinline__ void prefix_role(const DecodeParams& p, const Cascade
     step(I1{}, st + 1);
     if (st + 2 >= nstages) break;
     step(I2{}, st + 2);
-    if constexpr (NB == 4) {
-      if (st + 3 >= nstages) break;
-      step(I3{}, st + 3);
-    }
+    if (st + 3 >= nstages) break;
+    step(I3{}, st + 3);
   }
-
   }
 
   // Partial states: each row's true maximum, its weight sum against it and
