@@ -11,7 +11,9 @@
 //  * paged 5-D: K [nb, H, D/x, bs, x], V [nb, H, D, bs].  One wavefront per
 //    (token, head): K leaves as D/x 16-byte chunks at a stride of bs*16 bytes,
 //    V as D single elements at a stride of bs elements (the layout makes V
-//    token-minor, so its stores cannot be wider than one element).
+//    token-minor, so one token's stores cannot be wider than one element).
+//    Tokens that together fill a whole block in order (a prefill) instead
+//    write slices of the block's regions as whole lines (below).
 //  * FP8 caches (E4M3 codes of x / scale, either layout): see below.
 //  * token-major (MHATokenPool / flash): K and V [num_slots, H, D].  A token's
 //    K row and V row are each one contiguous H*D run in both source and
