@@ -476,6 +476,13 @@ def bench_splitk(dev, kernels, launches: int = 24):
                 method=f"HIP graph of {launches} calls over rotated pools, median of 5 replays")
 
 
+# GPU spin queued before each radix window.  After a churn step the GPU is
+# idle, and queueing four calls takes the host longer than the 80 us that a
+# single launch needs: with 80 us the first window after a churn held ~8 us
+# per launch of host time between the kernels.
+RADIX_SPIN_US = 400.0
+
+
 def bench_radix(dev, kernels, steps: int = 40, warmup: int = 5, layers: int = 4, fp8: bool = False):
     """Radix-shared decode (tests/pkv_workloads.py): 256 sequences (Llama-3-8B
     heads: 32 q / 8 kv, D128, bs16, bf16) whose block tables all start with
@@ -494,10 +501,10 @@ def bench_radix(dev, kernels, steps: int = 40, warmup: int = 5, layers: int = 4,
     w = RadixSharedWorkload(dev, kernels, layers=layers, fp8=fp8)
     # Each mode decodes right after a churn step of its own (the order of
     # the two modes alternates from step to step), then decodes the same
-    # step once more.  The first decode after the appends pays for the
-    # append's written lines still in the caches (measured 10-16 us per
-    # launch more than the second, whichever mode runs first), as a serving
-    # step would; the second is the decode alone.
+    # step once more.  The first decode after the appends pays for whatever
+    # the appends leave in the caches, as a serving step would; the second
+    # is the decode alone.  (With the appends' whole-block runs written as
+    # whole lines the two measure the same.)
     times = {(m, k): [] for m in ("cascade", "v1") for k in ("first", "second")}
 
     def launches(mode, info):
@@ -512,7 +519,10 @@ def bench_radix(dev, kernels, steps: int = 40, warmup: int = 5, layers: int = 4,
             info = w.churn()
             for k in ("first", "second"):
                 a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                queue_ahead()
+                # The host queues four calls (argument checks and, for the
+                # cascade, the plan's arrays) while the GPU spins: long
+                # enough that the window holds the kernels, not the host.
+                queue_ahead(RADIX_SPIN_US)
                 a.record()
                 launches(mode, info)
                 b.record()
