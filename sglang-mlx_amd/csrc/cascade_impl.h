@@ -495,12 +495,21 @@ __device__ __forceinline__ void prefix_role(const DecodeParams& p, const Cascade
           sc[4 + r] = (((lb >> r) & 1u) && vb + r < lim[s]) ? sc[4 + r] : -INFINITY;
         }
       }
-      float mt = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])), fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
-      mt = column_max(mt) * (plain ? cs : 1.f);  // log2 units
+      // The lane's maximum in log2 units (scaling by cs >= 0 commutes with
+      // the maximum exactly).  Over FP8 caches the column's is taken only
+      // when some lane passes the slack, off the path from the scores to the
+      // weights (radix-shared FP8 cascade 49.0 -> 48.2 us); over 16-bit
+      // caches in every pair, where the deferred form measured 0.6 us slower
+      // (67.5 against 68.1 us).  Either way reduce_max() at the end gives
+      // the column's maximum.
+      float ml =
+          fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])), fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
+      if constexpr (!PT::kF8) ml = column_max(ml);
+      ml *= plain ? cs : 1.f;
       WaveAcc<D>& a = acc[s];
-      a.m_max = fmaxf(a.m_max, mt);
-      if (__any(mt > a.m_run + kRescaleSlack)) {
-        const float m_new = fmaxf(a.m_run, mt);
+      a.m_max = fmaxf(a.m_max, ml);
+      if (__any(ml > a.m_run + kRescaleSlack)) {
+        const float m_new = fmaxf(a.m_run, PT::kF8 ? column_max(ml) : ml);
         const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(a.m_run - m_new);
         a.l_run *= alpha;
 #pragma unroll
@@ -549,12 +558,11 @@ __device__ __forceinline__ void prefix_role(const DecodeParams& p, const Cascade
   };
   // Direct-to-LDS loads a wavefront issues per stage; s_waitcnt immediates
   // (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt in 6:4 left at its
-  // maximum, lgkmcnt 0) that leave 0, 1 or 2 later stages' loads in flight.
+  // maximum, lgkmcnt 0) that leave 0 or 1 later stage's loads in flight.
   constexpr int LPS = PT::kKUnits / 64 * (BS >= kTile ? 1 : 2);
-  static_assert(2 * LPS < 64, "vmcnt counts at most 63 loads");
+  static_assert(LPS < 64, "vmcnt counts at most 63 loads");
   constexpr int kWait0 = (7 << 4);
   constexpr int kWait1 = (LPS & 15) | ((LPS >> 4) << 14) | (7 << 4);
-  constexpr int kWait2 = ((2 * LPS) & 15) | (((2 * LPS) >> 4) << 14) | (7 << 4);
   // The workgroup meets at a bare s_barrier (a __syncthreads, or any
   // workgroup fence that covers LDS, waits for every outstanding
   // direct-to-LDS load, the stages in flight included).  Each wavefront
@@ -677,6 +685,7 @@ __device__ __forceinline__ void prefix_role(const DecodeParams& p, const Cascade
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
     WaveAcc<D>& a = acc[s];
+    a.reduce_max();
     if (a.m_max != -INFINITY && a.m_max != a.m_run) {
       const float f = exp2f(a.m_run - a.m_max);
       a.l_run *= f;
@@ -743,6 +752,7 @@ __device__ __forceinline__ void tail_role(const DecodeParams& p, const CascadePa
       stream_tiles<QT, CT, D, BS, 1, MAXT, kTailBuffers>(p, kbase, vbase, blk, t0, t1, ctx, 0, g, col, qa, qb, slope,
                                                          acc);
     }
+    acc.reduce_max();
     if (acc.m_max != -INFINITY && acc.m_max != acc.m_run) {
       const float f = exp2f(acc.m_run - acc.m_max);
       acc.l_run *= f;

@@ -899,7 +899,12 @@ template <int BS, int MAXT> struct WaveBlocks {
 // One wavefront's softmax state: unnormalised output (MFMA accumulator
 // layout: lane l, register r of tile dt = head l%16, dim 16*dt + 4*(l/16) + r),
 // the reference maximum the weights are taken against, the weight sum of
-// this lane's 4 tokens per tile, and the true running maximum.
+// this lane's 4 tokens per tile, and the true running maximum.  While tiles
+// stream, m_max is the lane's own running maximum (over the scores it
+// holds); reduce_max() turns it into the column's, once, before it is read.
+// Keeping the cross-lane step out of the tile loop leaves it off every
+// tile's path from the scores to the weights: a tile needs the column
+// maximum only when some lane's scores pass the rescale slack.
 template <int D> struct WaveAcc {
   f32x4 o[Tile<D>::DT];
   float m_run, l_run, m_max;
@@ -910,6 +915,7 @@ template <int D> struct WaveAcc {
     l_run = 0.f;
     m_max = -INFINITY;
   }
+  __device__ __forceinline__ void reduce_max() { m_max = column_max(m_max); }
 };
 
 // Query rows h0 .. h0+nh-1 of sequence seq -> B-operand registers (head =
@@ -1031,10 +1037,12 @@ __device__ __forceinline__ void softmax_tile(const DecodeParams& p, f32x4 sacc, 
       for (int r = 0; r < 4; ++r) sc[r] = -INFINITY;
     }
   }
-  const float mt = column_max(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
-  acc.m_max = fmaxf(acc.m_max, mt);
-  if (__any(mt > acc.m_run + kRescaleSlack)) {
-    const float m_new = fmaxf(acc.m_run, mt);
+  // The lane's maximum decides whether any column passes the slack (m_run
+  // is the same in a column's four lanes); only then is the column's taken.
+  const float ml = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+  acc.m_max = fmaxf(acc.m_max, ml);
+  if (__any(ml > acc.m_run + kRescaleSlack)) {
+    const float m_new = fmaxf(acc.m_run, column_max(ml));
     const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(acc.m_run - m_new);
     acc.l_run *= alpha;
     // In place (each register multiplied where it lives): as a plain
@@ -1379,6 +1387,7 @@ __device__ __forceinline__ void merge_waves(WaveAcc<D>& acc, float (*s_red)[Tile
                                             float (*s_m)[16], float (*s_l)[16], int wave, int lane, int g, int col,
                                             float& M, float& L) {
   constexpr int DT = Tile<D>::DT;
+  acc.reduce_max();
   if (acc.m_max != -INFINITY && acc.m_max != acc.m_run) {
     const float f = exp2f(acc.m_run - acc.m_max);
     acc.l_run *= f;
@@ -1464,6 +1473,7 @@ __device__ __forceinline__ void merge_store_waves(const DecodeParams& p, WaveAcc
                                                   bool active) {
   using QS = typename Elem<QT>::storage;
   constexpr int DT = Tile<D>::DT;
+  acc.reduce_max();
   if (acc.m_max != -INFINITY && acc.m_max != acc.m_run) {
     const float f = exp2f(acc.m_run - acc.m_max);
     acc.l_run *= f;
