@@ -837,7 +837,14 @@ constexpr int kMergeRowWaves = 2;
 template <class QT, int D, int BS>
 __global__ __launch_bounds__(64 * kMergeRowWaves) void paged_cascade_merge_kernel(DecodeParams p, CascadeParams c) {
   using QS = typename Elem<QT>::storage;
-  constexpr int kStates = 6;  // states whose loads are in flight together
+  // States whose loads are in flight together: two while the early chunk
+  // states are still held (the tail partitions after the first), six after
+  // they are folded.  Six in both places kept 4 x 34 early registers live
+  // beside 6 x 34 loop registers (D = 128: 256 VGPRs plus 137 AGPR copies,
+  // now 256 + 14).  On the radix-shared workload (no row has more than the
+  // early states) the gain is at the noise level: FP8 cascade 47.5 -> 47.2
+  // us, bf16 68.0 -> 68.0 us (67.5 -> 67.3 us decoded again).
+  constexpr int kTailStates = 2, kChunkStates = 6;
   constexpr int DT = Tile<D>::DT;
   const int lane = threadIdx.x & 63;
   const int g = lane >> 4, col = lane & 15;
@@ -900,11 +907,11 @@ __global__ __launch_bounds__(64 * kMergeRowWaves) void paged_cascade_merge_kerne
   WaveAcc<D> acc;
   acc.init();
   if (on) fold_partial<D>(acc, ml_e[0].x, ml_e[0].y, o_e[0], g);
-  fold_states<D, kStates>(acc, c, row * c.max_parts + 1, nt - 1, 0, on ? nt - 1 : 0, g);
+  fold_states<D, kTailStates>(acc, c, row * c.max_parts + 1, nt - 1, 0, on ? nt - 1 : 0, g);
 #pragma unroll
   for (int e = 1; e <= kEarly; ++e)
     if (on && e - 1 < nch) fold_partial<D>(acc, ml_e[e].x, ml_e[e].y, o_e[e], g);
-  fold_states<D, kStates>(acc, c, 0, 0, row * c.max_chunks + kEarly, on ? nch - kEarly : 0, g);
+  fold_states<D, kChunkStates>(acc, c, 0, 0, row * c.max_chunks + kEarly, on ? nch - kEarly : 0, g);
   const float L = column_sum(acc.l_run);
   if (!on) return;
   const float inv = p.v_scale / (L + 1e-6f);
