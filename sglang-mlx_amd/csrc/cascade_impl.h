@@ -853,11 +853,14 @@ __global__ __launch_bounds__(64 * kMergeRowWaves) void paged_cascade_merge_kerne
   // role's workgroup for (tile, KV head h) has index = h mod 8 when there
   // are 8 KV heads, so XCD h wrote KV head h's prefix states.  With 8 KV
   // heads and a grid that is a multiple of 8, workgroup b takes row block
-  // (b mod 8) * grid/8 + b/8: XCD h merges KV head h's rows and finds their
-  // prefix states in its own L2 (radix-shared FP8 cascade 48.2 -> 47.4 us,
-  // bf16 68.3 -> 68.0 us; dealing the tail workgroups the same way measured
-  // 0.8 us slower on bf16).  Any other shape keeps the plain order; both are
-  // bijections onto the rows, and each row's fold order is the same.
+  // (b mod 8) * grid/8 + b/8, so that XCD h merges KV head h's rows.
+  // Measured in one process against the plain order: radix-shared FP8
+  // cascade 48.2 -> 47.4 us, bf16 68.3 -> 68.0 us per launch.  The merge
+  // kernel's L2 hit rate stays at 29% (per-XCD counters), so the gain is not
+  // its own L2 hits; where it comes from is not established.  (Dealing the
+  // tail workgroups the same way measured 0.8 us slower on bf16.)  Any other
+  // shape keeps the plain order; both are bijections onto the rows, and each
+  // row's fold order is the same.
   const int nblk = (int)gridDim.x, b = (int)blockIdx.x;
   const int lb = (p.num_kv_heads == 8 && nblk % 8 == 0) ? (b % 8) * (nblk / 8) + b / 8 : b;
   const int64_t r = ((int64_t)lb * kMergeRowWaves + (threadIdx.x >> 6)) * 16 + col;
