@@ -31,8 +31,8 @@
 //     sequence's prefix) through the one-sequence tile pipeline.  A
 //     sequence with no prefix and a single partition gets its output row
 //     written here; otherwise the partition's state goes to the workspace.
-// paged_cascade_merge_kernel -- one lane per (row, quarter of the head
-//   dimension) of the rows the tail role did not write: the row's tail
+// paged_cascade_merge_kernel -- sixteen lanes per row (D/16 dimensions
+//   each) of the rows the tail role did not write: the row's tail
 //   partitions' and prefix chunks' states folded by log-sum-exp in that
 //   fixed order, the row written.  States cross workgroups here, so they
 //   meet at the launch boundary rather than inside the first kernel, where
@@ -204,62 +204,83 @@ __device__ __forceinline__ uint32_t stage_part(uint4* dst, const typename Elem<C
 }
 
 
-// Folds one partial state (maximum m, weight sum l against it, unnormalised
-// output o of the lane's dimensions) into acc, whose m_run is its true
-// maximum.  The sum goes to the g == 0 lane of each column only: acc.l_run
-// holds per-lane parts that are summed over the column at the end.
+// The merge kernel's per-lane state: its row's running maximum and weight
+// sum (the same in each of the row's lanes, so no lane exchange is needed)
+// and the unnormalised output of the lane's NC four-dimension chunks
+// (dimensions 4 (e + 16 k) .. +3 for chunk k of lane e of the row).
+constexpr int kMergeLanesPerRow = 16;
+template <int D> struct MergeAcc {
+  static constexpr int NC = D / (4 * kMergeLanesPerRow);
+  float m, l;
+  float4 o[NC];
+};
+
+// Folds one partial state (maximum m, weight sum l against it, the lane's
+// chunks o of the unnormalised output) into acc, whose m is its true
+// maximum: acc rescaled onto max(acc.m, m), then the state added with
+// weight exp2(m - acc.m).  States whose maximum is -inf hold no tokens.
 template <int D>
-__device__ __forceinline__ void fold_partial(WaveAcc<D>& acc, float m, float l, const float4 (&o)[Tile<D>::DT],
-                                             int g) {
+__device__ __forceinline__ void fold_partial(MergeAcc<D>& acc, float m, float l, const float4 (&o)[MergeAcc<D>::NC]) {
   if (m == -INFINITY) return;
-  if (m > acc.m_run) {
-    const float f = acc.m_run == -INFINITY ? 0.f : exp2f(acc.m_run - m);
-    acc.l_run *= f;
+  if (m > acc.m) {
+    const float f = acc.m == -INFINITY ? 0.f : exp2f(acc.m - m);
+    acc.l *= f;
 #pragma unroll
-    for (int dt = 0; dt < Tile<D>::DT; ++dt) acc.o[dt] *= f;
-    acc.m_run = m;
+    for (int k = 0; k < MergeAcc<D>::NC; ++k) {
+      acc.o[k].x *= f;
+      acc.o[k].y *= f;
+      acc.o[k].z *= f;
+      acc.o[k].w *= f;
+    }
+    acc.m = m;
   }
-  const float w = exp2f(m - acc.m_run);
+  const float w = exp2f(m - acc.m);
 #pragma unroll
-  for (int dt = 0; dt < Tile<D>::DT; ++dt) {
-    acc.o[dt][0] += w * o[dt].x;
-    acc.o[dt][1] += w * o[dt].y;
-    acc.o[dt][2] += w * o[dt].z;
-    acc.o[dt][3] += w * o[dt].w;
+  for (int k = 0; k < MergeAcc<D>::NC; ++k) {
+    acc.o[k].x += w * o[k].x;
+    acc.o[k].y += w * o[k].y;
+    acc.o[k].z += w * o[k].z;
+    acc.o[k].w += w * o[k].w;
   }
-  if (g == 0) acc.l_run += w * l;
-  acc.m_max = acc.m_run;
+  acc.l += w * l;
+}
+
+// The lane's chunks of state slot `slot` of a workspace (ml: maxima and
+// sums, o: unnormalised outputs).
+template <int D>
+__device__ __forceinline__ void load_state(const float* ml, const float* o, int64_t slot, int e, float2& st_ml,
+                                           float4 (&st_o)[MergeAcc<D>::NC]) {
+  st_ml = *reinterpret_cast<const float2*>(ml + slot * 2);
+#pragma unroll
+  for (int k = 0; k < MergeAcc<D>::NC; ++k)
+    st_o[k] = *reinterpret_cast<const float4*>(o + slot * D + 4 * (e + kMergeLanesPerRow * k));
 }
 
 // Folds the n states of one row into acc, in order: tail partitions 0 ..
 // np-1 (ws_tail_*, slots tail0 + k), then prefix chunks (ws_*, slots
-// chunk0 + j); each lane its own row (n = 0 on lanes without one).  NB
-// states' loads are in flight at a time.
+// chunk0 + j); n = 0 on lanes without a row.  NB states' loads are in
+// flight at a time.
 template <int D, int NB>
-__device__ __forceinline__ void fold_states(WaveAcc<D>& acc, const CascadeParams& c, int64_t tail0, int np,
-                                            int64_t chunk0, int n, int g) {
-  constexpr int DT = Tile<D>::DT;
+__device__ __forceinline__ void fold_states(MergeAcc<D>& acc, const CascadeParams& c, int64_t tail0, int np,
+                                            int64_t chunk0, int n, int e) {
+  constexpr int NC = MergeAcc<D>::NC;
   for (int j0 = 0; j0 < n; j0 += NB) {
     float2 ml[NB];
-    float4 o[NB][DT];
+    float4 o[NB][NC];
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
       ml[b] = make_float2(-INFINITY, 0.f);
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) o[b][dt] = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int k = 0; k < NC; ++k) o[b][k] = make_float4(0.f, 0.f, 0.f, 0.f);
       const int j = j0 + b;
       if (j < n) {
         const bool tail = j < np;
-        const int64_t slot = tail ? tail0 + j : chunk0 + (j - np);
-        const float* wml = tail ? c.ws_tail_ml : c.ws_ml;
-        const float* wo = (tail ? c.ws_tail_o : c.ws_o) + slot * D + 4 * g;
-        ml[b] = *reinterpret_cast<const float2*>(wml + slot * 2);
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) o[b][dt] = *reinterpret_cast<const float4*>(wo + 16 * dt);
+        load_state<D>(tail ? c.ws_tail_ml : c.ws_ml, tail ? c.ws_tail_o : c.ws_o, tail ? tail0 + j : chunk0 + (j - np),
+                      e, ml[b], o[b]);
       }
     }
 #pragma unroll
-    for (int b = 0; b < NB; ++b) fold_partial<D>(acc, ml[b].x, ml[b].y, o[b], g);
+    for (int b = 0; b < NB; ++b) fold_partial<D>(acc, ml[b].x, ml[b].y, o[b]);
   }
 }
 
@@ -829,25 +850,29 @@ __global__ __launch_bounds__(64 * kCascadeWaves, 2) void paged_cascade_kernel(De
   }
 }
 
-// Rows of 16 per wavefront, kMergeRowWaves wavefronts per workgroup (two
-// measured 0.8 us faster on the FP8 radix-shared workload than one, and
-// the same over 16-bit caches; four were slower); lane (col, g) takes
-// quarter g of its wavefront's row col.
+// Four rows per wavefront (lane 16 rs + e: chunks of row rs), kMergeRowWaves
+// wavefronts per workgroup (with a quarter of the head dimension per lane,
+// two measured 0.8 us faster on the FP8 radix-shared workload than one, and
+// the same over 16-bit caches; four were slower).
 constexpr int kMergeRowWaves = 2;
+constexpr int kMergeRowsPerWave = 64 / kMergeLanesPerRow;
 template <class QT, int D, int BS>
 __global__ __launch_bounds__(64 * kMergeRowWaves) void paged_cascade_merge_kernel(DecodeParams p, CascadeParams c) {
   using QS = typename Elem<QT>::storage;
-  // States whose loads are in flight together: two while the early chunk
-  // states are still held (the tail partitions after the first), six after
-  // they are folded.  Six in both places kept 4 x 34 early registers live
-  // beside 6 x 34 loop registers (D = 128: 256 VGPRs plus 137 AGPR copies,
-  // now 256 + 14).  On the radix-shared workload (no row has more than the
-  // early states) the gain is at the noise level: FP8 cascade 47.5 -> 47.2
-  // us, bf16 68.0 -> 68.0 us (67.5 -> 67.3 us decoded again).
-  constexpr int kTailStates = 2, kChunkStates = 6;
-  constexpr int DT = Tile<D>::DT;
+  constexpr int NC = MergeAcc<D>::NC;
+  // States whose loads are in flight together after the early ones.
+  constexpr int kMoreStates = 4;
   const int lane = threadIdx.x & 63;
-  const int g = lane >> 4, col = lane & 15;
+  // Lane e of a row reads 16 bytes at 16 (e + 16 k) of each state's output:
+  // one load instruction covers 256 contiguous bytes of each of its rows.
+  // Sixteen lanes per row (122 VGPRs, four wavefronts per SIMD) against a
+  // quarter of the head dimension per lane (256 VGPRs plus AGPR copies, one
+  // wavefront per SIMD, and half the wavefronts): radix-shared FP8 cascade
+  // 47.4 -> 46.7 us, bf16 67.7 -> 67.5 us (eight lanes per row: 46.8 and
+  // 67.7 us), same process.  Each lane folds with the same operations in
+  // the same order as the quarter-per-lane form did (whose weight sums were
+  // summed over four lanes, three of them zero).
+  const int e = lane % kMergeLanesPerRow, rs = lane / kMergeLanesPerRow;
   // Rows go in KV-head-major order (KV head, sequence, head of the group).
   // Workgroups are dealt to the 8 XCDs round-robin by index, and the prefix
   // role's workgroup for (tile, KV head h) has index = h mod 8 when there
@@ -863,7 +888,7 @@ __global__ __launch_bounds__(64 * kMergeRowWaves) void paged_cascade_merge_kerne
   // row's fold order is the same.
   const int nblk = (int)gridDim.x, b = (int)blockIdx.x;
   const int lb = (p.num_kv_heads == 8 && nblk % 8 == 0) ? (b % 8) * (nblk / 8) + b / 8 : b;
-  const int64_t r = ((int64_t)lb * kMergeRowWaves + (threadIdx.x >> 6)) * 16 + col;
+  const int64_t r = ((int64_t)lb * kMergeRowWaves + (threadIdx.x >> 6)) * kMergeRowsPerWave + rs;
   bool on = r < (int64_t)p.num_seqs * p.num_heads;
   const int64_t per_kvh = (int64_t)p.num_seqs * p.group;  // rows per KV head
   const int64_t rr = on ? r : 0;
@@ -883,18 +908,12 @@ __global__ __launch_bounds__(64 * kMergeRowWaves) void paged_cascade_merge_kerne
   const uint32_t ctx = (uint32_t)p.context_lens[seq];
   const int plan_len = c.prefix_lens[seq];
   float2 ml_e[1 + kEarly];
-  float4 o_e[1 + kEarly][DT];
+  float4 o_e[1 + kEarly][NC];
   {
+    load_state<D>(c.ws_tail_ml, c.ws_tail_o, row * c.max_parts, e, ml_e[0], o_e[0]);
 #pragma unroll
-    for (int e = 0; e <= kEarly; ++e) {
-      const float* wml = e == 0 ? c.ws_tail_ml + row * c.max_parts * 2
-                                : c.ws_ml + (row * c.max_chunks + (e - 1 < c.max_chunks ? e - 1 : 0)) * 2;
-      const float* wo = e == 0 ? c.ws_tail_o + row * c.max_parts * D
-                               : c.ws_o + (row * c.max_chunks + (e - 1 < c.max_chunks ? e - 1 : 0)) * D;
-      ml_e[e] = *reinterpret_cast<const float2*>(wml);
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) o_e[e][dt] = *reinterpret_cast<const float4*>(wo + 4 * g + 16 * dt);
-    }
+    for (int j = 1; j <= kEarly; ++j)
+      load_state<D>(c.ws_ml, c.ws_o, row * c.max_chunks + (j - 1 < c.max_chunks ? j - 1 : 0), e, ml_e[j], o_e[j]);
     // No load may move past this asm (it may write memory), so all of them
     // are issued before the branches on the lengths; without it the
     // compiler moves the state loads into those branches.  It uses no
@@ -907,21 +926,23 @@ __global__ __launch_bounds__(64 * kMergeRowWaves) void paged_cascade_merge_kerne
   on = on && !(pre == 0 && np == 1);  // rows the tail role wrote
   const int nt = min(np, c.max_parts);  // >= 1
   const int nch = pre > 0 ? (pre + c.chunk - 1) / c.chunk : 0;  // <= max_chunks
-  WaveAcc<D> acc;
-  acc.init();
-  if (on) fold_partial<D>(acc, ml_e[0].x, ml_e[0].y, o_e[0], g);
-  fold_states<D, kTailStates>(acc, c, row * c.max_parts + 1, nt - 1, 0, on ? nt - 1 : 0, g);
+  MergeAcc<D> acc;
+  acc.m = -INFINITY;
+  acc.l = 0.f;
 #pragma unroll
-  for (int e = 1; e <= kEarly; ++e)
-    if (on && e - 1 < nch) fold_partial<D>(acc, ml_e[e].x, ml_e[e].y, o_e[e], g);
-  fold_states<D, kChunkStates>(acc, c, 0, 0, row * c.max_chunks + kEarly, on ? nch - kEarly : 0, g);
-  const float L = column_sum(acc.l_run);
+  for (int k = 0; k < NC; ++k) acc.o[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (on) fold_partial<D>(acc, ml_e[0].x, ml_e[0].y, o_e[0]);
+  fold_states<D, kMoreStates>(acc, c, row * c.max_parts + 1, nt - 1, 0, on ? nt - 1 : 0, e);
+#pragma unroll
+  for (int j = 1; j <= kEarly; ++j)
+    if (on && j - 1 < nch) fold_partial<D>(acc, ml_e[j].x, ml_e[j].y, o_e[j]);
+  fold_states<D, kMoreStates>(acc, c, 0, 0, row * c.max_chunks + kEarly, on ? nch - kEarly : 0, e);
   if (!on) return;
-  const float inv = p.v_scale / (L + 1e-6f);
+  const float inv = p.v_scale / (acc.l + 1e-6f);
   QS* out = static_cast<QS*>(p.out) + row * D;
 #pragma unroll
-  for (int dt = 0; dt < Tile<D>::DT; ++dt)
-    store4<QT>(out + 16 * dt + 4 * g, acc.o[dt][0] * inv, acc.o[dt][1] * inv, acc.o[dt][2] * inv, acc.o[dt][3] * inv);
+  for (int k = 0; k < NC; ++k)
+    store4<QT>(out + 4 * (e + kMergeLanesPerRow * k), acc.o[k].x * inv, acc.o[k].y * inv, acc.o[k].z * inv, acc.o[k].w * inv);
 }
 
 template <class QT, class CT, int D, int BS>
@@ -935,7 +956,7 @@ static hipError_t launch_cascade_bs(const DecodeParams& p, const CascadeParams& 
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int64_t rows = (int64_t)p.num_seqs * p.num_heads;
-  constexpr int kRowsPerGroup = 16 * kMergeRowWaves;
+  constexpr int kRowsPerGroup = kMergeRowsPerWave * kMergeRowWaves;
   hipLaunchKernelGGL((paged_cascade_merge_kernel<QT, D, BS>), dim3((unsigned)((rows + kRowsPerGroup - 1) / kRowsPerGroup)),
                      dim3(64 * kMergeRowWaves), 0, stream,
                      p, c);
