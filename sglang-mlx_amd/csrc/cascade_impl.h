@@ -210,6 +210,7 @@ __device__ __forceinline__ uint32_t stage_part(uint4* dst, const typename Elem<C
 // (dimensions 4 (e + 16 k) .. +3 for chunk k of lane e of the row).
 constexpr int kMergeLanesPerRow = 16;
 template <int D> struct MergeAcc {
+  static_assert(D % (4 * kMergeLanesPerRow) == 0, "whole four-dimension chunks per lane");
   static constexpr int NC = D / (4 * kMergeLanesPerRow);
   float m, l;
   float4 o[NC];
